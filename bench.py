@@ -1,0 +1,281 @@
+#!/usr/bin/env python
+"""Benchmark of the fused IQ3_S x MXFP8 projection on one MI355X.
+
+Default workload: the Llama-3-70B-shaped sweep - 80 layers x 7 projections (q 8192x8192,
+k/v 1024x8192, o 8192x8192, gate/up 28672x8192, down 8192x28672), 560 distinct IQ3_S
+weights (~29.4 GB resident in HBM) generated on the GPU from the counter-based
+generator, streamed once per step at M tokens (default M=1, decode). One step = the
+560 projections, launched from a captured HIP graph; MXFP8 activations are quantized
+once before timing (the reference times the matmul alone, iq3_s_fp8.py:402-465).
+
+value = algorithmic bytes per step / step time, with
+  bytes per projection = N*K*110/256 (IQ3_S weights) + M*K*33/32 (E4M3 + E8M0 activations)
+                         + 4*M*N (f32 output)
+roofline: HBM (8 TB/s) for the weight stream. cpu_baseline: the oracle's restatement of
+the reference CPU path (ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot) on
+BASELINE config 1 (N=K=4096, M=8), timed on this host.
+
+    python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+MXFP8_PEAK_TFLOPS = 5000.0
+
+LLAMA70B_LAYER = [("q", 8192, 8192, 0), ("k", 1024, 8192, 0), ("v", 1024, 8192, 0), ("o", 8192, 8192, 1),
+                  ("gate", 28672, 8192, 2), ("up", 28672, 8192, 2), ("down", 8192, 28672, 3)]
+LLAMA8B_SHAPES = [("q/o", 4096, 4096, 0), ("k/v", 1024, 4096, 0), ("gate/up", 14336, 4096, 0),
+                  ("down", 4096, 14336, 1)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def proj_bytes(m: int, n: int, k: int) -> int:
+    return n * k * 110 // 256 + m * k * 33 // 32 + 4 * m * n
+
+
+def synth_weight(n: int, k: int, seed: int):
+    import torch
+    from mambo_amd import _native
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    raw = torch.empty((n, k // 256, 110), dtype=torch.uint8, device="cuda")
+    _native.check(_native.lib().mambo_synth_iq3s(seed, k // 256, 0, n, raw.data_ptr(), _native.stream_handle(None)))
+    fields = prepare_iq3_s_fields(raw, fields=False)
+    del raw
+    return fields
+
+
+def synth_activation(m: int, k: int, seed: int):
+    import torch
+    from mambo_amd import _native
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    bits = torch.empty(m * k, dtype=torch.int16, device="cuda")
+    _native.check(_native.lib().mambo_synth_bf16(seed, 2, 0.0, 0, m * k, bits.data_ptr(), _native.stream_handle(None)))
+    return launch_quantize_fp8(bits.view(torch.bfloat16).view(m, k))
+
+
+def build_gemm_workload(args):
+    """Weights, activations, outputs and the launch list of the projection sweep."""
+    import torch
+    shapes = LLAMA70B_LAYER if args.workload == "llama70b" else LLAMA8B_SHAPES
+    layers = args.layers if args.workload == "llama70b" else args.copies
+    m = args.m
+    acts = {}
+    for _, n, k, slot in shapes:
+        if slot not in acts:
+            acts[slot] = synth_activation(m, k, seed=1 + slot)
+    outs = {}
+    launches = []
+    t0 = time.time()
+    for layer in range(layers):
+        for j, (name, n, k, slot) in enumerate(shapes):
+            fields = synth_weight(n, k, seed=1000 * layer + j)
+            key = (n, k)
+            if key not in outs:
+                outs[key] = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            launches.append((name, n, k, fields, acts[slot], outs[key]))
+        if layer % 10 == 9:
+            log(f"prepared {layer + 1}/{layers} layers ({time.time() - t0:.1f} s)")
+    torch.cuda.synchronize()
+    return launches
+
+
+def run_gemm(args):
+    import torch
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul, select_config
+
+    launches = build_gemm_workload(args)
+    configs = [select_config(args.m, n, k) for (_, n, k, _, _, _) in launches]
+    weight_bytes = sum(f.packed.numel() for (_, _, _, f, _, _) in launches)
+    step_bytes = sum(proj_bytes(args.m, n, k) for (_, n, k, _, _, _) in launches)
+    step_flops = sum(2 * args.m * n * k for (_, n, k, _, _, _) in launches)
+    log(f"{len(launches)} projections, {weight_bytes / 1e9:.2f} GB of IQ3_S weights resident")
+
+    def step():
+        for (_, _, _, fields, (xv, xs), out), cfg in zip(launches, configs):
+            launch_iq3_s_fp8_matmul(xv, xs, fields, config=cfg, out=out)
+
+    stream = torch.cuda.current_stream()
+    step()
+    torch.cuda.synchronize()
+    replay = step
+    if not args.no_graph:
+        # Capture one step on a side stream, then check one replay against eager results.
+        ref = {id(o): o.clone() for (_, _, _, _, _, o) in launches}
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                step()
+        stream.wait_stream(side)
+        for (_, _, _, _, _, o) in launches:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for (_, _, _, _, _, o) in launches:
+            if not torch.allclose(o, ref[id(o)], rtol=1e-5, atol=1e-6):
+                raise RuntimeError("graph replay differs from eager launch")
+        replay = graph.replay
+        log("captured the step in a HIP graph; replay matches eager")
+
+    for _ in range(args.warmup):
+        replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(stop) / args.steps
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    tflops = step_flops / (ms * 1e-3) / 1e12
+    log(f"{ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), {gbs:.1f} GB/s, {tflops:.2f} TFLOP/s")
+    return {
+        "ms": ms, "value": gbs, "tflops": tflops, "step_bytes": step_bytes, "step_flops": step_flops,
+        "weight_bytes": weight_bytes, "launches": len(launches),
+        "per_launch_bytes": step_bytes / len(launches), "per_launch_us": ms * 1e3 / len(launches),
+    }
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Oracle restatement of the reference CPU path on config 1: one IQ3_S linear
+    N=K=4096 (seed-0 counter-based blocks), M=8 bf16 ~N(0,1) activations quantized to
+    MXFP8, IQ3_S to_float + float64-accumulated dot per output (all host cores)."""
+    import numpy as np
+    from oracle import oracle
+    n = k = 4096
+    m = 8
+    raw = oracle.gen_iq3s(0, n, k // 256)
+    xv, xs = oracle.quantize_mxfp8(oracle.gen_bf16(1, m * k).reshape(m, k))
+    threads = len(os.sched_getaffinity(0))
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        oracle.iq3s_fp8_matmul(xv, xs, raw, threads=threads)
+        iters += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    per = (time.perf_counter() - t0) / iters
+    gbs = proj_bytes(m, n, k) / per / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"BASELINE config 1: N=K=4096, M=8, {iters} runs in {per * iters:.1f} s "
+                      f"({per * 1e3:.1f} ms each) of the oracle's to_float + f64-dot restatement "
+                      f"of ggml_reference.cpp:495-523 on {threads} threads"}
+
+
+def run_quant(args):
+    import torch
+    from mambo_amd import _native
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    m = k = 4096
+    copies = 8  # rotate 8 x 32 MiB inputs so the 256 MB MALL does not hold them
+    xs = []
+    for c in range(copies):
+        bits = torch.empty(m * k, dtype=torch.int16, device="cuda")
+        _native.check(_native.lib().mambo_synth_bf16(1 + c, 2, 0.001, 0, m * k, bits.data_ptr(),
+                                                     _native.stream_handle(None)))
+        xs.append(bits.view(torch.bfloat16).view(m, k))
+    outs = [(torch.empty((m, k), dtype=torch.uint8, device="cuda"),
+             torch.empty((m, k // 32), dtype=torch.uint8, device="cuda")) for _ in range(copies)]
+    for i in range(args.warmup * copies):
+        launch_quantize_fp8(xs[i % copies], out=outs[i % copies])
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    n = args.steps * copies
+    for i in range(n):
+        launch_quantize_fp8(xs[i % copies], out=outs[i % copies])
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / n
+    nbytes = m * k * (2 + 1) + m * (k // 32)
+    return {"ms": ms, "value": nbytes / (ms * 1e-3) / 1e9, "step_bytes": nbytes, "launches": 1,
+            "per_launch_bytes": nbytes, "per_launch_us": ms * 1e3}
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--m", type=int, default=1, help="tokens per projection")
+    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant"], default="llama70b")
+    p.add_argument("--layers", type=int, default=80, help="llama70b: layers in the sweep")
+    p.add_argument("--copies", type=int, default=48, help="llama8b: distinct weight copies per shape")
+    p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        return 2
+    rank = int(os.environ.get("RANK", "0"))
+
+    import torch
+    from mambo_amd import _native
+    _native.lib()
+    log(f"device {torch.cuda.get_device_name(0)} ({_native.device_arch()})")
+
+    if args.workload == "quant":
+        r = run_quant(args)
+        metric = "MXFP8 activation quantizer GB/s (bf16 [4096,4096] -> E4M3 + E8M0)"
+        workload = "mxfp8 quantize bf16 [4096,4096], 0.1% x100 outliers, 8 rotated inputs"
+        config = {"workload": workload, "m": 4096, "k": 4096}
+    else:
+        r = run_gemm(args)
+        metric = "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline"
+        if args.workload == "llama70b":
+            workload = f"llama3-70b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}"
+        else:
+            workload = f"llama3-8b projection shapes x {args.copies} rotated copies, M={args.m}"
+        config = {"workload": workload, "m": args.m, "projections_per_step": r["launches"],
+                  "weight_gb": round(r["weight_bytes"] / 1e9, 3), "tflops": round(r["tflops"], 3),
+                  "graph": not args.no_graph}
+    value = r["value"]
+    line = {
+        "metric": metric,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 x iq3_s, f32 accumulate",
+        "data": "synthetic (counter-based IQ3_S blocks, bf16 ~N(0,1) activations)",
+        "config": config,
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": round(r["per_launch_bytes"]),
+                     "avg_launch_us": round(r["per_launch_us"], 3)},
+    }
+    if rank == 0 and not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if rank == 0:
+        print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,163 @@
+/*
+ * libmambo_hip: C ABI of the MI355X (gfx950) fused IQ3_S x MXFP8 projection path.
+ *
+ * Conventions
+ *   - Every pointer argument named as a tensor is a device pointer owned by the
+ *     caller; the library never allocates or frees caller memory and never
+ *     synchronises the host. Work is ordered on `stream` (NULL = default stream).
+ *   - Strides (ld*) count elements of the pointed-to type.
+ *   - Return value: MAMBO_OK (0) or a negative MAMBO_ERR_* class; the message is
+ *     available from mambo_last_error() on the calling thread. No C++ exception
+ *     crosses this boundary. The Python layer maps ERR_VALUE -> ValueError,
+ *     ERR_TYPE -> TypeError, everything else -> RuntimeError, as the reference
+ *     launchers raise them.
+ *
+ * Each entry point names the reference interface it replaces (paths are in the
+ * Menooker/Mambo reference). The reference launches cuTile kernels with
+ * ct.launch(stream, grid, kernel, args); its AOT ABI (cutile_to_cubin.py:83-95)
+ * expands every array into (ptr, shape..., stride...). This ABI passes the same
+ * data as plain pointers, sizes and row strides.
+ */
+#ifndef MAMBO_HIP_H
+#define MAMBO_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *mambo_stream_t; /* == hipStream_t */
+
+enum {
+    MAMBO_OK = 0,
+    MAMBO_ERR_VALUE = -1,       /* bad shape, dtype, stride, alignment or config */
+    MAMBO_ERR_TYPE = -2,        /* wrong kind of argument (e.g. unprepared weight) */
+    MAMBO_ERR_RUNTIME = -3,     /* HIP runtime / launch failure */
+    MAMBO_ERR_UNSUPPORTED = -4  /* device is not gfx950 */
+};
+
+enum { MAMBO_DTYPE_F32 = 0, MAMBO_DTYPE_BF16 = 1 };
+
+/* Kernel families of the projection. */
+enum {
+    MAMBO_GEMM_AUTO = 0,    /* library default for the shape */
+    MAMBO_GEMM_STREAM = 1,  /* weight-streaming split-K kernel, M-chunks of 16 */
+    MAMBO_GEMM_TILED = 2    /* LDS-tiled kernel for large M */
+};
+
+/* Tunable launch configuration of mambo_iq3s_fp8_matmul (the autotuner's search
+ * space; replaces the cuTile tile_m/tile_n/split_k/occupancy hints of
+ * iq3_s_fp8.py:49-58,402-465). Zero fields (and kernel == MAMBO_GEMM_AUTO) take the
+ * value of mambo_gemm_default_config for the shape. */
+typedef struct mambo_gemm_config {
+    int32_t kernel;  /* MAMBO_GEMM_* */
+    int32_t waves;   /* waves (64 lanes) per workgroup */
+    int32_t split_k; /* workgroups sharing one output tile along K (f32 atomics) */
+    int32_t tile_m;  /* TILED: rows of M per workgroup */
+    int32_t tile_n;  /* TILED: rows of N per workgroup */
+    int32_t reserved[3];
+} mambo_gemm_config;
+
+/* Last error message of the calling thread ("" if none). */
+const char *mambo_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+int mambo_abi_version(void);
+
+/* Architecture the device code was built for ("gfx950"). */
+const char *mambo_build_arch(void);
+
+/* Writes the gcnArchName of `device` (e.g. "gfx950:sramecc+:xnack-") into buf. */
+int mambo_device_arch(int device, char *buf, int buf_len);
+
+/* Host copies of the codebook: iq3s_grid (iq3_s_fp8.py:63-74, `iq3_s_table`) and its
+ * E4M3-encoded form (iq3_s_fp8.py:77-94, `iq3_s_fp8_table`). out: uint32[512]. */
+int mambo_iq3s_grid(uint32_t *out);
+int mambo_iq3s_fp8_grid(uint32_t *out);
+
+/* MXFP8 activation quantizer. Replaces launch_quantize_fp8 / quantize_activation_fp8
+ * (quantize_fp8.py:42-52,67-84). x: [m, ldx] of f32 or bf16 (x_dtype); per 32
+ * consecutive K elements writes one E8M0 scale byte (scales[m, lds]) and 32 E4M3
+ * bytes (values[m, ldv]): e = max(ceil(log2(amax/448)), -127) computed exactly
+ * (0 for an all-zero block), q = E4M3(x * 2^-e) with round-to-nearest-even.
+ * k % 32 == 0; m >= 1. */
+int mambo_quantize_mxfp8(const void *x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                         uint8_t *values, int64_t ldv, uint8_t *scales, int64_t lds,
+                         mambo_stream_t stream);
+
+/* Bytes of the private tile layout for an [n, blocks] IQ3_S weight. */
+int64_t mambo_iq3s_packed_bytes(int64_t n, int64_t blocks);
+
+/* Split raw GGUF IQ3_S blocks into the reference's SoA fields and/or the private tile
+ * layout. Replaces prepare_iq3_s_fields (iq3_s_weight.py:25-54). raw byte (r, b, i) is
+ * at raw + r*stride_n + b*stride_b + i*stride_byte (any alignment). Outputs (each may
+ * be NULL, but not all): d u16[blocks, n], qs u32[blocks, n, 16], qh u16[blocks, n, 4],
+ * signs i32[blocks, n, 8], scales u32[blocks, n] (IQ3SFields, iq3_s_weight.py:10-23),
+ * packed u8[mambo_iq3s_packed_bytes(n, blocks)]. */
+int mambo_iq3s_prepare(const uint8_t *raw, int64_t n, int64_t blocks, int64_t stride_n,
+                       int64_t stride_b, int64_t stride_byte, uint16_t *d, uint32_t *qs,
+                       uint16_t *qh, int32_t *signs, uint32_t *scales, uint8_t *packed,
+                       mambo_stream_t stream);
+
+/* Build the tile layout from SoA fields (for IQ3SFields built by other means). */
+int mambo_iq3s_pack(const uint16_t *d, const uint32_t *qs, const uint16_t *qh,
+                    const int32_t *signs, const uint32_t *scales, int64_t n, int64_t blocks,
+                    uint8_t *packed, mambo_stream_t stream);
+
+/* Standalone decoder. Replaces launch_dequant_iq3_s / decode_iq3_s_blocks
+ * (iq3_s_fp8.py:202-222,341-351): values u8[n, blocks*256] = E4M3 bits of
+ * sign * grid magnitude, out_scales f32[n, blocks*8] = f32(d) * (1 + 2*s). */
+int mambo_iq3s_dequant(const uint16_t *d, const uint32_t *qs, const uint16_t *qh,
+                       const int32_t *signs, const uint32_t *scales, int64_t n, int64_t blocks,
+                       uint8_t *values, float *out_scales, mambo_stream_t stream);
+
+/* Fused projection out[m, n] (f32, row stride ldo) = sum over K of
+ * MXFP8(x)[m, k] * IQ3_S(w)[n, k]. Replaces launch_iq3_s_fp8_matmul with
+ * iq3_s_fp8_matmul / iq3_s_fp8_matmul_medium (iq3_s_fp8.py:225-333,364-399).
+ * xv u8[m, ldxv] E4M3, xs u8[m, ldxs] E8M0 (K = blocks*256, K/32 scales per row);
+ * packed: tile layout from mambo_iq3s_prepare/mambo_iq3s_pack.
+ * xv and ldxv must be 16-byte aligned. cfg may be NULL (library default). When the
+ * chosen configuration splits K, `out` is zeroed on `stream` first and partial sums are
+ * added with f32 atomics (results then vary in the last bits from run to run, as the
+ * reference's split-K does). */
+int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
+                          int64_t m, const uint8_t *packed, int64_t n, int64_t blocks,
+                          float *out, int64_t ldo, const mambo_gemm_config *cfg,
+                          mambo_stream_t stream);
+
+/* The configuration mambo_iq3s_fp8_matmul uses when cfg == NULL. */
+int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out);
+
+/* Validates cfg for the shape (MAMBO_OK or MAMBO_ERR_VALUE with a reason). */
+int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, const mambo_gemm_config *cfg);
+
+/* Synthetic inputs for benchmarks and full-size checks (no reference counterpart; the
+ * reference draws them with numpy/cupy RNGs, test_iq3_s_fp8.py:41-51). Counter-based:
+ *   rnd(seed, stream, i) = splitmix64(splitmix64(seed*0xD1B54A32D192ED03 + stream) + i);
+ *   normal(seed, stream, i) = (sum_{t<12} (rnd(seed, stream, 12i+t) >> 32) - 6*2^32) / 2^32.
+ * mambo_synth_iq3s: raw u8[nrows, blocks, 110] for weight rows [row0, row0+nrows):
+ *   bytes 2..109 of block (r, b) = bytes of rnd(seed, 1, 14*(r*blocks+b) + j/8);
+ *   d = fp16(f32(|normal(seed, 2, r*blocks+b)| * 2e-3)).
+ * mambo_synth_bf16: out[i] = bf16(f32(normal(seed, 3, i0+i) * (outlier ? 100 : 1))),
+ *   outlier iff (rnd(outlier_seed, 4, i0+i) >> 11) < outlier_frac * 2^53. */
+int mambo_synth_iq3s(uint64_t seed, int64_t blocks, int64_t row0, int64_t nrows, uint8_t *raw,
+                     mambo_stream_t stream);
+int mambo_synth_bf16(uint64_t seed, uint64_t outlier_seed, double outlier_frac, int64_t i0,
+                     int64_t count, uint16_t *out, mambo_stream_t stream);
+
+/* Diagnostic: element-wise f32 -> E4M3 through the kernels' integer rounding path
+ * (out_sw) and the hardware v_cvt_pk_fp8_f32 (out_hw); either output may be NULL.
+ * Used to check the hardware conversion against the integer restatement. */
+int mambo_e4m3_convert(const float *in, int64_t n, uint8_t *out_sw, uint8_t *out_hw,
+                       mambo_stream_t stream);
+
+/* Fill n floats with `value` (a kernel, not hipMemsetAsync, so it may be captured in
+ * a HIP graph). */
+int mambo_fill_f32(float *ptr, int64_t n, float value, mambo_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBO_HIP_H */

@@ -1,0 +1,362 @@
+// Fused IQ3_S x MXFP8 projection for gfx950: out[m, n] = sum_k x[m, k] * w[n, k].
+//
+// Reference semantics (src/python/mambo/kernels/iq3_s_fp8.py:225-333): per 32-weight
+// group, an FP8 block-scaled MMA of the E4M3 activation codes (E8M0 scale per
+// activation group) with the E4M3 grid magnitudes (weight scale 1.0), then the f32
+// post-scale F = d * (1 + 2*nibble) of the weight group, accumulated over groups.
+//
+// Streaming kernel (this file, all M; one pass over the weights per 16 rows of M).
+// One wave owns a 16-row weight tile and walks super-blocks along K; the workgroup's
+// waves split the blocks of one K range and reduce through LDS; several workgroups may
+// split K further (f32 atomics into a zeroed output).
+//
+// Per super-block each lane decodes 16 four-weight codes (groups 2q and 2q+1 of row
+// col, q = lane/16, col = lane%16) straight into the B operand of
+// V_MFMA_SCALE_F32_16X16X128_F8F6F4: lane l of B holds K chunk q (32 bytes) of column
+// col, so one lane's decoded group is exactly its B slice; nothing decoded touches HBM.
+//   code address: 2 VALU (funnel shift + mask of the 9-bit index stream)
+//   magnitude:    1 LDS read of the E4M3-encoded grid word
+//   signs:        2 VALU (rotate the bit-transposed sign word, bit-field insert)
+// Because F differs per 32-weight group and a K=128 MFMA spans four groups, the A
+// operand (activations) is block-diagonal: row i = 4*g' + m' of A holds activation row
+// m' only in K chunk g' (zero elsewhere). Output row (g', m') of lane l then carries the
+// partial dot product of exactly the group lane l decoded, so each lane post-scales its
+// own accumulator by its own group's F; the four g' partials are summed at the end.
+// M up to 4 per MFMA, up to 16 per pass (U = 1..4 MFMAs per K step).
+#include "mambo_common.h"
+
+namespace {
+
+__constant__ GridTables c_grid = kGridTables;
+
+// Operands of lanes outside the block-diagonal activation tile: 64 zero bytes and two
+// unit E8M0 scales (2^0).
+// Kept in the global address space (not constant) so the activation pointers stay
+// global and the loads are global_load, not flat_load.
+__device__ __align__(16) uint8_t g_zero_chunk[64] = {};
+__device__ uint8_t g_unit_scales[2] = {127, 127};
+
+
+struct WTile {
+    uint4 ia;     // idx stream bits 0..127
+    uint16_t ib;  // idx stream bits 128..143
+    uint2 sg;     // transposed sign words, groups 2q and 2q+1
+    uint8_t sc;   // scale nibbles of groups 2q, 2q+1
+    uint16_t dh;  // fp16 d of row col
+};
+
+__device__ __forceinline__ WTile load_w(const uint8_t *__restrict__ tb, int lane, int col)
+{
+    WTile w;
+    w.ia = *reinterpret_cast<const uint4 *>(tb + kTileIdxA + 16 * lane);
+    w.ib = *reinterpret_cast<const uint16_t *>(tb + kTileIdxB + 2 * lane);
+    w.sg = *reinterpret_cast<const uint2 *>(tb + kTileSigns + 8 * lane);
+    w.sc = tb[kTileScales + lane];
+    w.dh = *reinterpret_cast<const uint16_t *>(tb + kTileD + 2 * col);
+    return w;
+}
+
+// Byte address (idx << 2) of code I's grid word; idx = bits [9I, 9I+9) of the stream.
+template <int I>
+__device__ __forceinline__ uint32_t code_addr(const uint32_t (&s)[5])
+{
+    constexpr int p = 9 * I - 2;
+    if constexpr (p < 0) {
+        return (s[0] << 2) & 0x7FCu;
+    } else {
+        constexpr int wi = p >> 5, sh = p & 31;
+        if constexpr (wi + 1 <= 4)
+            return funnel_shr(s[wi + 1], s[wi], sh) & 0x7FCu;
+        else
+            return (s[wi] >> sh) & 0x7FCu;
+    }
+}
+
+// Signed E4M3 word of code C (0..7) of a group: grid magnitudes with the four sign
+// bits of the code moved onto bits 7, 15, 23, 31 by one rotate of the transposed word.
+template <int C>
+__device__ __forceinline__ uint32_t signed_word(uint32_t mag, uint32_t p)
+{
+    const uint32_t rot = funnel_shr(p, p, (25 + C) & 31);
+    return (rot & 0x80808080u) | mag;
+}
+
+template <int H, int... C>
+__device__ __forceinline__ v8i decode_group(const uint32_t (&s)[5], uint32_t p, const uint8_t *lut,
+                                            std::integer_sequence<int, C...>)
+{
+    v8i b;
+    ((b[C] = (int)signed_word<C>(*reinterpret_cast<const uint32_t *>(lut + code_addr<8 * H + C>(s)), p)), ...);
+    return b;
+}
+
+template <int U>
+struct ATile {
+    v8i a[U][2];
+    uint8_t s[U][2];
+};
+
+// Activation slices of one super-block. Lanes outside the block-diagonal (and rows
+// past M) read a zero buffer with a zero stride, so every load is unconditional.
+struct ALane {
+    const uint8_t *x;  // activation bytes of this lane's chunk, block 0
+    const uint8_t *s;  // E8M0 scale of this lane's chunk, block 0
+    int64_t xstep;     // 256 or 0
+    int64_t sstep;     // 8 or 0
+};
+
+template <int U>
+__device__ __forceinline__ void load_a(ATile<U> &at, const ALane (&al)[U], int b)
+{
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint8_t *xp = al[u].x + (int64_t)b * al[u].xstep;
+        const uint8_t *sp = al[u].s + (int64_t)b * al[u].sstep;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(xp + 32 * h);
+            const uint4 lo = p[0], hi = p[1];
+            at.a[u][h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            at.s[u][h] = sp[h];
+        }
+    }
+}
+
+template <int U>
+__device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at, const uint8_t *lut, float (&acc)[U][4])
+{
+    const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
+    const float d = half_bits_to_float((uint16_t)w.dh);
+    const v8i b0 = decode_group<0>(s, w.sg.x, lut, std::make_integer_sequence<int, 8>{});
+    const v8i b1 = decode_group<1>(s, w.sg.y, lut, std::make_integer_sequence<int, 8>{});
+    const uint32_t sc = w.sc;
+    const float f0 = d * (float)(1u + 2u * (sc & 15u));
+    const float f1 = d * (float)(1u + 2u * (sc >> 4));
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        v4f c0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][0], b0, zero, 0, 0, 0, (int)at.s[u][0], 0, 127);
+        v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][1], b1, zero, 0, 0, 0, (int)at.s[u][1], 0, 127);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[u][r] = __builtin_fmaf(c1[r], f1, __builtin_fmaf(c0[r], f0, acc[u][r]));
+    }
+}
+
+template <int U, int W>
+__global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
+                                                             const uint8_t *__restrict__ packed, int64_t N, int B,
+                                                             int bps, float *__restrict__ out, int64_t ldo, int atomic)
+{
+    __shared__ uint32_t lut_words[512];
+    __shared__ float red[W][U * 4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: scalar loop control
+    for (int i = tid; i < 512; i += W * 64)
+        lut_words[i] = c_grid.fp8[i];
+    __syncthreads();
+    const uint8_t *lut = reinterpret_cast<const uint8_t *>(lut_words);
+
+    const int64_t t = blockIdx.x;
+    const int b_begin = blockIdx.y * bps;
+    const int b_end = min(B, b_begin + bps);
+    const int64_t m0 = (int64_t)blockIdx.z * 16;
+    const int col = lane & 15, q = lane >> 4;
+    const bool a_lane = (col >> 2) == q;
+
+    ALane al[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t m = m0 + 4 * u + (lane & 3);
+        const bool on = a_lane && m < M;
+        al[u].x = on ? xv + m * ldxv + 64 * q : g_zero_chunk;
+        al[u].s = on ? xs + m * ldxs + 2 * q : g_unit_scales;
+        al[u].xstep = on ? 256 : 0;
+        al[u].sstep = on ? 8 : 0;
+    }
+
+    float acc[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[u][r] = 0.0f;
+
+    const uint8_t *wt = packed + t * (int64_t)B * kTileBytes;
+    // Blocks of this wave: b_begin + wave, + W, ... (count is wave-uniform).
+    const int first = b_begin + wave;
+    const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
+    if (count > 0) {
+        // Two register sets used in turn; each loop trip decodes exactly two blocks while
+        // the next one is in flight. The prefetch after the last pair re-reads a block
+        // of this wave (a cache hit) so every load is unconditional and stays ahead of
+        // its use. An odd final block is decoded after the loop.
+        const int last = first + (count - 1) * W;
+        int b = first;
+        WTile w0 = load_w(wt + (int64_t)b * kTileBytes, lane, col), w1;
+        ATile<U> a0, a1;
+        load_a<U>(a0, al, b);
+        for (int pair = 0; pair < count / 2; ++pair) {
+            w1 = load_w(wt + (int64_t)(b + W) * kTileBytes, lane, col);
+            load_a<U>(a1, al, b + W);
+            compute_block<U>(w0, a0, lut, acc);
+            const int b2 = min(b + 2 * W, last);
+            w0 = load_w(wt + (int64_t)b2 * kTileBytes, lane, col);
+            load_a<U>(a0, al, b2);
+            compute_block<U>(w1, a1, lut, acc);
+            b += 2 * W;
+        }
+        if (count & 1)
+            compute_block<U>(w0, a0, lut, acc);
+    }
+
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            red[wave][u * 4 + r][lane] = acc[u][r];
+    __syncthreads();
+    for (int i = tid; i < U * 4 * 16; i += W * 64) {
+        const int ur = i >> 4, c = i & 15;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq)
+                v += red[w][ur][qq * 16 + c];
+        const int64_t m = m0 + ur, n = t * kTileRows + c;
+        if (m < M && n < N) {
+            float *o = out + m * ldo + n;
+            if (atomic)
+                atomicAdd(o, v);
+            else
+                *o = v;
+        }
+    }
+}
+
+__global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t cols, int64_t ld)
+{
+    const int64_t r = blockIdx.y;
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += (int64_t)gridDim.x * blockDim.x)
+        out[r * ld + c] = 0.0f;
+    (void)rows;
+}
+
+template <int U, int W>
+void launch_stream_uw(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
+                      int64_t M, const uint8_t *packed, int64_t N, int B, int bps, float *out, int64_t ldo, int atomic)
+{
+    hipLaunchKernelGGL((gemm_stream_kernel<U, W>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs, ldxs, M, packed, N, B,
+                       bps, out, ldo, atomic);
+}
+
+template <int U>
+int launch_stream_u(int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
+                    int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B, int bps, float *out, int64_t ldo,
+                    int atomic)
+{
+    switch (waves) {
+    case 1: launch_stream_uw<U, 1>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
+    case 2: launch_stream_uw<U, 2>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
+    case 4: launch_stream_uw<U, 4>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
+    case 8: launch_stream_uw<U, 8>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
+    default: return mambo_fail(MAMBO_ERR_VALUE, "waves must be 1, 2, 4 or 8 (got %d)", waves);
+    }
+    return MAMBO_OK;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+} // namespace
+
+extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out)
+{
+    MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
+    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
+    mambo_gemm_config c = {};
+    c.kernel = MAMBO_GEMM_STREAM;
+    c.waves = 4;
+    const int64_t tiles = cdiv(n, kTileRows) * cdiv(m, 16);
+    // Aim for >= 2 workgroups of 4 waves per CU (256 CUs) with >= 2 blocks per wave.
+    int64_t split = cdiv(512, tiles);
+    const int64_t max_split = std::max<int64_t>(1, blocks / (2 * c.waves));
+    split = std::min<int64_t>(std::max<int64_t>(split, 1), max_split);
+    c.split_k = (int32_t)split;
+    *out = c;
+    return MAMBO_OK;
+}
+
+extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, const mambo_gemm_config *cfg)
+{
+    MAMBO_REQUIRE(cfg != nullptr, MAMBO_ERR_VALUE, "cfg must not be NULL");
+    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
+    MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM, MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
+    MAMBO_REQUIRE(cfg->waves == 1 || cfg->waves == 2 || cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE,
+                  "waves must be 1, 2, 4 or 8");
+    MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
+                  "split_k must be in [1, K/256]");
+    return MAMBO_OK;
+}
+
+extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t m,
+                                     const uint8_t *packed, int64_t n, int64_t blocks, float *out, int64_t ldo,
+                                     const mambo_gemm_config *cfg, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(xv && xs && packed && out, MAMBO_ERR_VALUE, "null pointer");
+    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive (M=%lld N=%lld B=%lld)",
+                  (long long)m, (long long)n, (long long)blocks);
+    MAMBO_REQUIRE(blocks <= 0x7FFFFFFF / 8, MAMBO_ERR_VALUE, "K too large");
+    const int64_t k = blocks * 256;
+    MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32 && ldo >= n, MAMBO_ERR_VALUE, "row strides must cover the row");
+    MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
+                  "x_values base and row stride must be 16-byte aligned");
+    MAMBO_REQUIRE((uintptr_t)packed % 16 == 0, MAMBO_ERR_VALUE, "packed weight must be 16-byte aligned");
+    // Library default for the shape, overlaid with the non-zero fields of cfg.
+    mambo_gemm_config c;
+    int rc = mambo_gemm_default_config(m, n, blocks, &c);
+    if (rc)
+        return rc;
+    if (cfg != nullptr) {
+        if (cfg->kernel != MAMBO_GEMM_AUTO)
+            c.kernel = cfg->kernel;
+        if (cfg->waves)
+            c.waves = cfg->waves;
+        if (cfg->split_k)
+            c.split_k = cfg->split_k;
+        if (cfg->tile_m)
+            c.tile_m = cfg->tile_m;
+        if (cfg->tile_n)
+            c.tile_n = cfg->tile_n;
+        rc = mambo_gemm_check_config(m, n, blocks, &c);
+        if (rc)
+            return rc;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t tiles = cdiv(n, kTileRows);
+    const int64_t mchunks = cdiv(m, 16);
+    MAMBO_REQUIRE(tiles <= 0x7FFFFFFF && mchunks <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
+    const int bps = (int)cdiv(blocks, c.split_k);
+    const int splits = (int)cdiv(blocks, bps);
+    const int atomic = splits > 1;
+    if (atomic) {
+        dim3 zg((unsigned)std::min<int64_t>(cdiv(n, 256), 1024), (unsigned)m);
+        MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
+        hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, out, m, n, ldo);
+        rc = mambo_check_launch("zero_rows");
+        if (rc)
+            return rc;
+    }
+    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
+    const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
+    switch (U) {
+    case 1: rc = launch_stream_u<1>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    case 2: rc = launch_stream_u<2>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    case 3: rc = launch_stream_u<3>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    default: rc = launch_stream_u<4>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    }
+    if (rc)
+        return rc;
+    return mambo_check_launch("iq3s_fp8_matmul");
+}

@@ -1,0 +1,126 @@
+// Shared definitions for the gfx950 kernels of libmambo_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mambo_hip.h"
+#include "iq3s_grid.h"
+
+// ----------------------------------------------------------------------------- errors
+// Thread-local last error (api.cpp). Entry points return a MAMBO_* status.
+int mambo_fail(int status, const char *fmt, ...);
+int mambo_check_launch(const char *what);
+
+#define MAMBO_REQUIRE(cond, status, ...)                                                           \
+    do {                                                                                           \
+        if (!(cond))                                                                               \
+            return mambo_fail((status), __VA_ARGS__);                                              \
+    } while (0)
+
+// ----------------------------------------------------------------------------- IQ3_S layout
+// One IQ3_S super-block: 256 weights in 110 bytes (iq3_s_fp8.py:11-21).
+constexpr int kIq3sBlockBytes = 110;
+constexpr int kIq3sBlockValues = 256;
+
+// Private tile layout written by mambo_iq3s_prepare/mambo_iq3s_pack and read by the
+// projection kernels. One tile = 16 weight rows x one super-block = 1760 bytes,
+// tiles ordered [row_tile][block]. Lane l of a 64-lane wave (col = l & 15 = row in the
+// tile, q = l >> 4) owns groups 2q and 2q+1 of its row:
+//   [   0, 1024)  idx stream, bits 0..127 of lane l at 16*l   (dwordx4 per lane)
+//   [1024, 1152)  idx stream, bits 128..143 of lane l at 2*l
+//   [1152, 1664)  sign words of groups 2q, 2q+1 of lane l at 8*l, bit-transposed
+//   [1664, 1728)  scale byte of lane l: low nibble group 2q, high nibble group 2q+1
+//   [1728, 1760)  fp16 d of row col at 2*col
+// idx stream: code i (0..15, codes 16q..16q+15 of the row) occupies bits [9i, 9i+9) and
+// holds qs | qh_bit << 8. Transposed sign word P of a group: bit (c + 8j) of P is the
+// sign of weight 4c+j, so one rotate places code c's four signs on bits 7,15,23,31.
+// The bytes are a permutation of the 16 source blocks' bytes (16 x 110 = 1760).
+constexpr int kTileRows = 16;
+constexpr int kTileBytes = kTileRows * kIq3sBlockBytes;
+constexpr int kTileIdxA = 0;
+constexpr int kTileIdxB = 1024;
+constexpr int kTileSigns = 1152;
+constexpr int kTileScales = 1664;
+constexpr int kTileD = 1728;
+static_assert(kTileD + 2 * kTileRows == kTileBytes, "tile layout must be byte-preserving");
+
+// E4M3 (OCP, bias 7) encodings of the odd grid magnitudes 1,3,...,15 (iq3_s_fp8.py:80-81).
+__host__ __device__ constexpr uint32_t e4m3_of_odd(uint32_t m)
+{
+    return m == 1 ? 0x38u : m == 3 ? 0x44u : m == 5 ? 0x4Au : m == 7 ? 0x4Eu : m == 9 ? 0x51u
+         : m == 11 ? 0x53u : m == 13 ? 0x55u : m == 15 ? 0x57u : 0xFFu;
+}
+
+struct GridTables {
+    uint32_t raw[512];   // magnitudes 1..15 per byte
+    uint32_t fp8[512];   // E4M3 bits of the magnitudes (iq3_s_fp8_table)
+    uint32_t level[512]; // (magnitude - 1) / 2 per byte: 0..7
+};
+
+__host__ __device__ constexpr GridTables make_grid_tables()
+{
+    GridTables t{{MAMBO_IQ3S_GRID_WORDS}, {}, {}};
+    for (int i = 0; i < 512; ++i) {
+        uint32_t f = 0, l = 0;
+        for (int j = 0; j < 4; ++j) {
+            uint32_t m = (t.raw[i] >> (8 * j)) & 0xFFu;
+            f |= e4m3_of_odd(m) << (8 * j);
+            l |= ((m - 1u) / 2u) << (8 * j);
+        }
+        t.fp8[i] = f;
+        t.level[i] = l;
+    }
+    return t;
+}
+
+inline constexpr GridTables kGridTables = make_grid_tables();
+
+// ----------------------------------------------------------------------------- device helpers
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t funnel_shr(uint32_t hi, uint32_t lo, uint32_t s)
+{
+    return __builtin_amdgcn_alignbit(hi, lo, s);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h)
+{
+    _Float16 v = __builtin_bit_cast(_Float16, h);
+    return (float)v;
+}
+
+// Exact MXFP8 block exponent (quantize_fp8.py:32-38 with an exact ceil(log2(amax/448))):
+// amax = m * 2^E, m in [1,2): e = E-8 if m <= 1.75 else E-7; 0 for amax == 0;
+// clamped to [-127, 127]. Subnormal amax always gives -127.
+__device__ __forceinline__ int mxfp8_exponent(float amax)
+{
+    uint32_t u = __float_as_uint(amax);
+    if (u == 0u)
+        return 0;
+    if (u < 0x00800000u)
+        return -127;
+    int E = (int)(u >> 23) - 127;
+    int e = ((u & 0x7FFFFFu) <= 0x600000u) ? E - 8 : E - 7;
+    return e < -127 ? -127 : e;
+}
+
+// |y| <= 448 (or any finite y: saturating) -> E4M3 bits, round to nearest even,
+// sign of y kept (including -0). Integer restatement of the OCP conversion.
+__device__ __forceinline__ uint32_t e4m3_rne_sw(float y)
+{
+    uint32_t u = __float_as_uint(y);
+    uint32_t sign = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7FFFFFFFu;
+    uint32_t code;
+    if (a < 0x3C800000u) { // < 2^-6: subnormal grid, step 2^-9
+        float q = __builtin_rintf(__uint_as_float(a) * 512.0f);
+        code = (uint32_t)q; // 0..8; 8 is the smallest normal
+    } else {
+        uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);
+        code = (r >> 20) - (120u << 3);
+        code = code > 0x7Eu ? 0x7Eu : code;
+    }
+    return sign | code;
+}

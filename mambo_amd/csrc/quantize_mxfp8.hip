@@ -1,0 +1,179 @@
+// MXFP8 activation quantizer for gfx950.
+//
+// Semantics follow the reference kernel quantize_fp8_group / quantize_activation_fp8
+// (src/python/mambo/kernels/quantize_fp8.py:23-52): per 32 consecutive K elements of a
+// row, amax -> e = max(ceil(log2(amax/448)), -127) (e = 0 when amax == 0), one E8M0
+// scale byte e+127 and 32 E4M3 codes of x * 2^-e rounded to nearest even. The exponent
+// is computed exactly from the bits of amax instead of through f32 log2.
+//
+// Mapping: four lanes per 32-element group, eight elements per lane, so every
+// wave-wide load and store instruction covers one contiguous span (bf16: 1 KiB per
+// load). amax is reduced across the quad with two lane swaps. The kernel is HBM-bound:
+// M*K*(in_bytes + 1 + 1/32) bytes per call.
+#include "mambo_common.h"
+
+namespace {
+
+// E4M3 rounding path of the quantizer: hardware v_cvt_pk_fp8_f32 (true) or the integer
+// restatement e4m3_rne_sw (false).
+constexpr bool kQuantHwCvt = false;
+
+template <bool kBf16>
+__device__ __forceinline__ void load8(const void *__restrict__ x, int64_t off, float v[8])
+{
+    if constexpr (kBf16) {
+        uint4 r = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + off);
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + off);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+}
+
+template <bool kBf16>
+__device__ __forceinline__ void load8_scalar(const void *__restrict__ x, int64_t off, float v[8])
+{
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if constexpr (kBf16)
+            v[i] = __uint_as_float((uint32_t)(reinterpret_cast<const uint16_t *>(x)[off + i]) << 16);
+        else
+            v[i] = reinterpret_cast<const float *>(x)[off + i];
+    }
+}
+
+// Four E4M3 codes packed little-endian.
+template <bool kHw>
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d)
+{
+    if constexpr (kHw) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+        return (uint32_t)w;
+    } else {
+        return e4m3_rne_sw(a) | (e4m3_rne_sw(b) << 8) | (e4m3_rne_sw(c) << 16) | (e4m3_rne_sw(d) << 24);
+    }
+}
+
+template <bool kBf16, bool kVec, bool kHw>
+__global__ __launch_bounds__(256) void quantize_mxfp8_kernel(const void *__restrict__ x, int64_t ldx,
+                                                             int64_t m, int64_t groups,
+                                                             uint8_t *__restrict__ values, int64_t ldv,
+                                                             uint8_t *__restrict__ scales, int64_t lds)
+{
+    const int64_t g = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+    const int j = threadIdx.x & 3;
+    const bool ok = g < groups;
+    for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
+        float v[8];
+        if (ok) {
+            const int64_t off = row * ldx + 32 * g + 8 * j;
+            if constexpr (kVec)
+                load8<kBf16>(x, off, v);
+            else
+                load8_scalar<kBf16>(x, off, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[i] = 0.0f;
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            amax = fmaxf(amax, fabsf(v[i]));
+        // quad reduction: lanes 4t..4t+3 hold one group
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const int e = mxfp8_exponent(amax);
+        if (ok) {
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                y[i] = __builtin_ldexpf(v[i], -e); // exact scaling by a power of two
+            uint2 out;
+            out.x = pack4<kHw>(y[0], y[1], y[2], y[3]);
+            out.y = pack4<kHw>(y[4], y[5], y[6], y[7]);
+            uint8_t *vp = values + row * ldv + 32 * g + 8 * j;
+            if constexpr (kVec) {
+                *reinterpret_cast<uint2 *>(vp) = out;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    vp[i] = (uint8_t)(out.x >> (8 * i));
+                    vp[4 + i] = (uint8_t)(out.y >> (8 * i));
+                }
+            }
+            if (j == 0)
+                scales[row * lds + g] = (uint8_t)(e + 127);
+        }
+    }
+}
+
+// Element-wise E4M3 conversion with the software and the hardware rounding paths, for
+// checking the hardware conversion against the integer restatement.
+__global__ void e4m3_convert_kernel(const float *__restrict__ in, int64_t n, uint8_t *__restrict__ sw,
+                                    uint8_t *__restrict__ hw)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    float v = in[i];
+    if (sw)
+        sw[i] = (uint8_t)e4m3_rne_sw(v);
+    if (hw)
+        hw[i] = (uint8_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false);
+}
+
+template <bool kBf16, bool kVec>
+int launch(const void *x, int64_t m, int64_t groups, int64_t ldx, uint8_t *values, int64_t ldv,
+           uint8_t *scales, int64_t lds, hipStream_t stream)
+{
+    dim3 grid((unsigned)((groups + 63) / 64), (unsigned)(m < 65535 ? m : 65535));
+    hipLaunchKernelGGL((quantize_mxfp8_kernel<kBf16, kVec, kQuantHwCvt>), grid, dim3(256), 0, stream,
+                       x, ldx, m, groups, values, ldv, scales, lds);
+    return mambo_check_launch("quantize_mxfp8");
+}
+
+} // namespace
+
+extern "C" int mambo_quantize_mxfp8(const void *x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                                    uint8_t *values, int64_t ldv, uint8_t *scales, int64_t lds,
+                                    mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(x_dtype == MAMBO_DTYPE_F32 || x_dtype == MAMBO_DTYPE_BF16, MAMBO_ERR_VALUE,
+                  "activation dtype must be float32 or bfloat16");
+    MAMBO_REQUIRE(m >= 1 && k >= 32 && k % 32 == 0, MAMBO_ERR_VALUE,
+                  "activation must be [M,K] with M >= 1 and K divisible by 32 (got M=%lld K=%lld)",
+                  (long long)m, (long long)k);
+    MAMBO_REQUIRE(ldx >= k && ldv >= k && lds >= k / 32, MAMBO_ERR_VALUE, "row strides must cover K");
+    MAMBO_REQUIRE(x && values && scales, MAMBO_ERR_VALUE, "null pointer");
+    const int64_t groups = k / 32;
+    MAMBO_REQUIRE((groups + 63) / 64 <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "K too large");
+    const size_t esz = x_dtype == MAMBO_DTYPE_BF16 ? 2 : 4;
+    const bool vec = ((uintptr_t)x % 16 == 0) && ((ldx * (int64_t)esz) % 16 == 0) &&
+                     ((uintptr_t)values % 8 == 0) && (ldv % 8 == 0);
+    hipStream_t s = (hipStream_t)stream;
+    if (x_dtype == MAMBO_DTYPE_BF16)
+        return vec ? launch<true, true>(x, m, groups, ldx, values, ldv, scales, lds, s)
+                   : launch<true, false>(x, m, groups, ldx, values, ldv, scales, lds, s);
+    return vec ? launch<false, true>(x, m, groups, ldx, values, ldv, scales, lds, s)
+               : launch<false, false>(x, m, groups, ldx, values, ldv, scales, lds, s);
+}
+
+extern "C" int mambo_e4m3_convert(const float *in, int64_t n, uint8_t *out_sw, uint8_t *out_hw,
+                                  mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(n >= 0 && in != nullptr, MAMBO_ERR_VALUE, "bad input");
+    if (n == 0)
+        return MAMBO_OK;
+    hipLaunchKernelGGL(e4m3_convert_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       in, n, out_sw, out_hw);
+    return mambo_check_launch("e4m3_convert");
+}

@@ -1,0 +1,226 @@
+"""IQ3_S block decode and block-scaled FP8 projection on gfx950.
+
+Mirror of src/python/mambo/kernels/iq3_s_fp8.py. The projection reads prepared IQ3_S
+weights (IQ3SFields) and prequantized MXFP8 activations and decodes the IQ3_S blocks
+inside the GEMM tile; the decoded weights never reach HBM. A standalone decoder serves
+independent correctness checks. The kernels are hand-written HIP for gfx950
+(mambo_amd/csrc/iq3s_gemm.hip, iq3s_layout.hip) behind the C ABI.
+
+One IQ3_S block along K (256 weights, 110 bytes):
+
+    byte  0..1   | d: FP16 base scale                 |  2 bytes
+    byte  2..65  | qs: 64 low 8-bit codebook indices  | 64 bytes
+    byte 66..73  | qh: 64 high index bits             |  8 bytes
+    byte 74..105 | signs: one bit per weight          | 32 bytes
+    byte 106..109| scales: 8 packed 4-bit values      |  4 bytes
+
+Each 9-bit (qs, qh) index selects four magnitudes from the codebook; each group of 32
+weights uses scale d * (1 + 2 * scale_nibble).
+"""
+
+from __future__ import annotations
+
+import json
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from mambo_amd import _native
+from mambo_amd.utils.iq3_s_weight import (
+    IQ3SFields,
+    IQ3_S_BLOCK_BYTES,
+    IQ3_S_BLOCK_VALUES,
+    _weight_dimensions,
+    _weight_kernel_args,
+    ensure_packed,
+    prepare_iq3_s_fields,
+)
+
+IQ3_S_SCALE_VALUES = 32
+_IQ3_TABLES: dict[int, torch.Tensor] = {}
+
+# Launch configurations per architecture, selected by token count as in the reference
+# (iq3_s_fp8.py:49-60). Fields follow mambo_gemm_config; 0 = library default for the
+# shape. Per-shape autotuned entries (tuned_gfx950.json, written by
+# mambo_amd.utils.kernel_benchmark) take precedence.
+BEST_CONFIGS = {
+    "gfx950": {
+        "medium": {"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 0},
+        "large": {"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 0},
+    },
+}
+LARGE_TOKEN_THRESHOLD = 32
+TUNED_PATH = Path(__file__).resolve().parent / "tuned_gfx950.json"
+
+
+@lru_cache(maxsize=1)
+def _tuned_table() -> dict:
+    if TUNED_PATH.exists():
+        return json.loads(TUNED_PATH.read_text())
+    return {}
+
+
+def m_bucket(m: int) -> int:
+    """Token-count bucket of the tuned table: the next power of two >= m."""
+    return 1 << max(0, (int(m) - 1).bit_length())
+
+
+def tuned_key(n: int, k: int, m: int) -> str:
+    return f"{n}x{k}@{m_bucket(m)}"
+
+
+@lru_cache(maxsize=1)
+def iq3_s_table() -> np.ndarray:
+    """The 512-entry IQ3_S codebook (iq3s_grid), four magnitudes per uint32."""
+    out = np.zeros(512, dtype=np.uint32)
+    _native.check(_native.lib().mambo_iq3s_grid(out.ctypes.data), "iq3_s_table")
+    if out.shape != (512,):
+        raise ValueError(f"expected 512 IQ3_S table entries, got {out.size}")
+    return out
+
+
+@lru_cache(maxsize=1)
+def iq3_s_fp8_table() -> np.ndarray:
+    """Pack positive magnitudes as E4M3 bits (iq3_s_fp8.py:77-94)."""
+    magnitudes = np.array([1, 3, 5, 7, 9, 11, 13, 15], dtype=np.uint8)
+    fp8_bits = np.array([0x38, 0x44, 0x4A, 0x4E, 0x51, 0x53, 0x55, 0x57], dtype=np.uint8)
+    lookup = np.zeros(256, dtype=np.uint8)
+    valid = np.zeros(256, dtype=np.bool_)
+    lookup[magnitudes] = fp8_bits
+    valid[magnitudes] = True
+    raw_table = iq3_s_table()
+    encoded_table = np.zeros_like(raw_table)
+    for shift in (0, 8, 16, 24):
+        magnitude = (raw_table >> shift) & 0xFF
+        if not np.all(valid[magnitude]):
+            raise ValueError("IQ3_S codebook contains a magnitude without an E4M3 encoding")
+        encoded_table |= lookup[magnitude].astype(np.uint32) << shift
+    return encoded_table
+
+
+def _get_iq3_table() -> torch.Tensor:
+    """FP8-encoded codebook on the current device (iq3_s_fp8.py:97-102). The kernels
+    carry their own copy in the code object; this tensor is for callers that want it."""
+    device = torch.cuda.current_device()
+    if device not in _IQ3_TABLES:
+        _IQ3_TABLES[device] = torch.from_numpy(iq3_s_fp8_table().view(np.int32)).to(f"cuda:{device}")
+    return _IQ3_TABLES[device]
+
+
+def _power_of_two(value: int, name: str) -> None:
+    if value < 1 or value & (value - 1):
+        raise ValueError(f"{name} must be a positive power of two")
+
+
+def launch_dequant_iq3_s(iq3_weight: IQ3SFields, *, tile_n: int = 1, stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Return [N,K] E4M3 bit patterns and [N,K/32] original F32 scales (iq3_s_fp8.py:341-351).
+
+    ``tile_n`` is validated (power of two) as in the reference; the gfx950 decoder's
+    launch shape does not depend on it.
+    """
+    _power_of_two(tile_n, "tile_n")
+    n_rows, blocks = _weight_dimensions(iq3_weight)
+    fields = _weight_kernel_args(iq3_weight)
+    for name, t in zip(("d", "qs", "qh", "signs", "scales"), fields):
+        if not t.is_contiguous() or t.numel() == 0 and n_rows * blocks:
+            raise ValueError(f"IQ3SFields.{name} must be a contiguous prepared field")
+    dev = iq3_weight.d.device
+    values = torch.empty((n_rows, blocks * 256), dtype=torch.uint8, device=dev)
+    scales = torch.empty((n_rows, blocks * 8), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().mambo_iq3s_dequant(*(t.data_ptr() for t in fields), n_rows, blocks,
+                                                       values.data_ptr(), scales.data_ptr(),
+                                                       _native.stream_handle(stream)), "launch_dequant_iq3_s")
+    return values, scales
+
+
+def select_config(m: int, n: int, k: int, arch: str | None = None) -> dict:
+    """Launch configuration for an [M, K] x [N, K] projection on `arch`."""
+    arch = arch or _native.device_arch()
+    if arch not in BEST_CONFIGS:
+        raise RuntimeError(f"IQ3_S FP8 matmul has no tuned config for {arch}")
+    tuned = _tuned_table().get(arch, {}).get(tuned_key(n, k, m))
+    if tuned is not None:
+        return dict(tuned)
+    return dict(BEST_CONFIGS[arch]["medium" if m < LARGE_TOKEN_THRESHOLD else "large"])
+
+
+def launch_iq3_s_fp8_matmul(x_values: torch.Tensor, x_scales: torch.Tensor, iq3_weight: IQ3SFields,
+                            *, stream=None, config: dict | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Multiply prepared IQ3_S weights by prequantized MXFP8 activations (iq3_s_fp8.py:364-399).
+
+    x_values uint8 [M,K] (E4M3), x_scales uint8 [M,K/32] (E8M0); returns float32 [M,N].
+    Row-strided activations are read in place; a non-unit column stride (or a row
+    stride that is not a multiple of 16 bytes) is copied first. ``config`` overrides
+    the tuned launch configuration (mambo_gemm_config fields); ``out`` optionally
+    supplies the float32 [M,N] output (unit column stride).
+    """
+    n_rows, k_blocks = _weight_dimensions(iq3_weight)
+    k = k_blocks * IQ3_S_BLOCK_VALUES
+    if not isinstance(x_values, torch.Tensor) or x_values.ndim != 2 or x_values.dtype != torch.uint8 \
+            or x_values.shape[0] < 1 or x_values.shape[1] != k:
+        raise ValueError("x_values must be uint8 [M,K]")
+    m = int(x_values.shape[0])
+    if not isinstance(x_scales, torch.Tensor) or tuple(x_scales.shape) != (m, k // 32) \
+            or x_scales.dtype != torch.uint8:
+        raise ValueError("x_scales must be uint8 [M,K/32]")
+    dev = x_values.device
+    with torch.cuda.device(dev):
+        cfg = _native.GemmConfig.from_dict(config if config is not None else select_config(m, n_rows, k))
+        packed = ensure_packed(iq3_weight, stream)
+        if x_values.stride(1) != 1 or x_values.stride(0) % 16 or x_values.data_ptr() % 16:
+            x_values = x_values.contiguous() if x_values.stride(1) != 1 else x_values.clone()
+        if x_scales.stride(1) != 1:
+            x_scales = x_scales.contiguous()
+        if out is None:
+            out = torch.empty((m, n_rows), dtype=torch.float32, device=dev)
+        elif tuple(out.shape) != (m, n_rows) or out.dtype != torch.float32 or out.stride(1) != 1:
+            raise ValueError("out must be float32 [M,N] with unit column stride")
+        _native.check(_native.lib().mambo_iq3s_fp8_matmul(
+            x_values.data_ptr(), x_values.stride(0), x_scales.data_ptr(), x_scales.stride(0), m,
+            packed.data_ptr(), n_rows, k_blocks, out.data_ptr(), out.stride(0), cfg,
+            _native.stream_handle(stream)), "launch_iq3_s_fp8_matmul")
+    return out
+
+
+def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
+    """Candidate launch configurations for the autotuner (the analogue of the cuTile
+    search spaces of iq3_s_fp8.py:416-459): waves per workgroup x K split."""
+    blocks = k // IQ3_S_BLOCK_VALUES
+    space = []
+    for waves in (1, 2, 4, 8):
+        for split in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
+            if split <= blocks and (blocks + split - 1) // split >= 1:
+                space.append({"kernel": _native.GEMM_STREAM, "waves": waves, "split_k": split})
+    return space
+
+
+def make_benchmark_cases(iq3_weight: torch.Tensor, tokens: tuple[int, ...] = (4, 128)) -> list:
+    """Prepare weights and MXFP8 inputs once; benchmark only the projection
+    (iq3_s_fp8.py:402-465). ``iq3_weight`` is raw GGUF uint8 [N,B,110] on the GPU."""
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    from mambo_amd.utils.kernel_benchmark import BenchmarkCase
+
+    fields = prepare_iq3_s_fields(iq3_weight)
+    n_rows, k_blocks = _weight_dimensions(fields)
+    k = k_blocks * IQ3_S_BLOCK_VALUES
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=iq3_weight.device)
+    gen.manual_seed(0)
+
+    def make_case(m: int):
+        x = torch.randn((m, k), dtype=torch.float32, device=iq3_weight.device, generator=gen)
+        x_values, x_scales = launch_quantize_fp8(x, stream=stream)
+        out = torch.empty((m, n_rows), dtype=torch.float32, device=iq3_weight.device)
+
+        def launch(config):
+            launch_iq3_s_fp8_matmul(x_values, x_scales, fields, stream=stream, config=config, out=out)
+
+        return BenchmarkCase(name=f"M={m} N={n_rows} K={k}", stream=stream, launch=launch,
+                             search_space=gemm_search_space(m, n_rows, k), summary_keys=("waves", "split_k"),
+                             key=tuned_key(n_rows, k, m))
+
+    return [make_case(m) for m in tokens]

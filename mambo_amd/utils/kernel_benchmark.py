@@ -1,0 +1,213 @@
+"""Autotuning and benchmark command for the gfx950 projection kernels.
+
+Mirror of src/python/mambo/utils/kernel_benchmark.py: each kernel module supplies
+benchmark cases; this module searches each case's launch configurations, re-times the
+winner with the reference's three timers (mean_us with a sync per launch, batched_us,
+event_us; 5 warm-up and 20 iterations, kernel_benchmark.py:56-94) and reports it.
+
+    python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --model M.gguf --weight-name NAME
+    python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --synthetic 4096 4096 [--write-table]
+
+The reference copies winners into BEST_CONFIGS by hand (kernels/AGENTS.md:27); here
+``--write-table`` stores them per shape in mambo_amd/kernels/tuned_gfx950.json, which
+launch_iq3_s_fp8_matmul consults first.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+from dataclasses import dataclass, field
+from pathlib import Path
+from time import perf_counter
+from typing import Any, Callable, Sequence
+
+import numpy as np
+import torch
+
+from mambo_amd.utils.gguf import inspect_gguf
+
+Config = dict[str, Any]
+
+
+@dataclass(frozen=True)
+class BenchmarkCase:
+    name: str
+    stream: Any
+    launch: Callable[[Config], None]
+    search_space: Sequence[Config]
+    summary_keys: tuple[str, ...] = ()
+    # Per-invocation state reset, included in reported timings after tuning.
+    before_launch_fn: Callable[[Config], None] | None = None
+    key: str = ""
+
+
+@dataclass
+class TuneResult:
+    case: str
+    key: str
+    best: Config
+    mean_us: float
+    batched_us: float
+    event_us: float
+    tuner_us: float
+    successes: list = field(default_factory=list)
+    failures: list = field(default_factory=list)
+
+
+def _time_events(stream, fn, iters: int) -> float:
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) * 1000.0 / iters
+
+
+def exhaustive_search(case: BenchmarkCase, *, warmup: int = 2, iters: int = 10):
+    """Time every configuration of the case; failures (invalid configs) are recorded."""
+    successes, failures = [], []
+    for config in case.search_space:
+        def once(config=config):
+            if case.before_launch_fn is not None:
+                case.before_launch_fn(config)
+            case.launch(config)
+        try:
+            for _ in range(warmup):
+                once()
+            torch.cuda.synchronize()
+            us = _time_events(case.stream, once, iters)
+            successes.append((config, us))
+        except (ValueError, RuntimeError) as exc:
+            failures.append((config, str(exc)))
+    if not successes:
+        raise RuntimeError(f"{case.name}: no configuration ran ({failures[:3]})")
+    return successes, failures
+
+
+def mini_benchmark(cases: Sequence[BenchmarkCase], *, quiet: bool = False) -> list[TuneResult]:
+    """Tune each case, then time the winner with any per-launch reset (kernel_benchmark.py:41-100)."""
+    results = []
+    for case in cases:
+        successes, failures = exhaustive_search(case)
+        best, tuner_us = min(successes, key=lambda item: item[1])
+
+        def launch_once() -> None:
+            if case.before_launch_fn is not None:
+                case.before_launch_fn(best)
+            case.launch(best)
+
+        def measure(*, batched: bool) -> float:
+            for _ in range(5):
+                launch_once()
+                if not batched:
+                    case.stream.synchronize()
+            if batched:
+                case.stream.synchronize()
+            start = perf_counter()
+            for _ in range(20):
+                launch_once()
+                if not batched:
+                    case.stream.synchronize()
+            if batched:
+                case.stream.synchronize()
+            return (perf_counter() - start) * 1e6 / 20
+
+        mean_us = measure(batched=False)
+        batched_us = measure(batched=True)
+        event_us = _time_events(case.stream, launch_once, 20)
+        result = TuneResult(case.name, case.key, dict(best), mean_us, batched_us, event_us, tuner_us,
+                            successes, failures)
+        results.append(result)
+        if not quiet:
+            print(f"{case.name}: best_config={best}, "
+                  f"mean_us={mean_us:.3f}, batched_us={batched_us:.3f}, "
+                  f"event_us={event_us:.3f}, "
+                  f"tuner_us={tuner_us:.3f} (warmup=5, iterations=20), "
+                  f"candidates={len(successes)} passed/{len(failures)} failed")
+            if case.summary_keys:
+                by_group: dict[tuple[Any, ...], float] = {}
+                for config, us in successes:
+                    group = tuple(config[key] for key in case.summary_keys)
+                    by_group[group] = min(by_group.get(group, float("inf")), us)
+                print(f"  best latency by {case.summary_keys} (us): {by_group}")
+    return results
+
+
+def write_tuned_table(results: Sequence[TuneResult], path: Path, arch: str) -> None:
+    table = json.loads(path.read_text()) if path.exists() else {}
+    entries = table.setdefault(arch, {})
+    for r in results:
+        if r.key:
+            entries[r.key] = r.best
+    path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
+
+
+def load_gguf_weight(model: Path, weight_name: str, expected_type: str) -> torch.Tensor:
+    """Load a named 2D packed GGUF tensor as [N, K/block_elements, block_bytes] on the GPU
+    (kernel_benchmark.py:103-122)."""
+    manifest = inspect_gguf(model)
+    tensor = next((item for item in manifest["tensors"] if item["name"] == weight_name), None)
+    if tensor is None:
+        raise ValueError(f"GGUF has no tensor named {weight_name!r}")
+    quant_type = tensor["type"]
+    if quant_type["name"] != expected_type or len(tensor["shape"]) != 2:
+        raise ValueError(f"{weight_name} must be a 2D {expected_type} tensor")
+    k, n_rows = tensor["shape"]
+    block_values = quant_type["block_elements"]
+    block_bytes = quant_type["block_bytes"]
+    if (not block_values or not block_bytes or k % block_values
+            or tensor["row_bytes"] != k // block_values * block_bytes
+            or tensor["n_bytes"] != n_rows * tensor["row_bytes"]):
+        raise ValueError(f"{weight_name} has an inconsistent GGUF block layout")
+    raw = np.memmap(model, mode="r", dtype=np.uint8, offset=tensor["offset"]["absolute"],
+                    shape=(n_rows, k // block_values, block_bytes))
+    return torch.from_numpy(np.ascontiguousarray(raw)).cuda()
+
+
+def synthetic_weight(n: int, k: int, seed: int = 0) -> torch.Tensor:
+    """Random IQ3_S blocks u8 [N, K/256, 110] generated on the GPU (counter-based)."""
+    from mambo_amd import _native
+    raw = torch.empty((n, k // 256, 110), dtype=torch.uint8, device="cuda")
+    _native.check(_native.lib().mambo_synth_iq3s(seed, k // 256, 0, n, raw.data_ptr(),
+                                                 _native.stream_handle(None)), "synth_iq3s")
+    return raw
+
+
+# Add a kernel module and an entry here for each new benchmark.
+_BENCHMARKS = {
+    "iq3_s_fp8": ("iq3_s", "mambo_amd.kernels.iq3_s_fp8", "make_benchmark_cases"),
+}
+
+
+def benchmark_main(argv: Sequence[str] | None = None) -> list[TuneResult]:
+    parser = argparse.ArgumentParser(description="Autotune a gfx950 projection kernel")
+    parser.add_argument("kernel", choices=sorted(_BENCHMARKS))
+    parser.add_argument("--model", type=Path, help="GGUF model path")
+    parser.add_argument("--weight-name", help="tensor name in the GGUF model")
+    parser.add_argument("--synthetic", nargs=2, type=int, metavar=("N", "K"),
+                        help="use a random IQ3_S weight of this shape instead of a GGUF tensor")
+    parser.add_argument("--tokens", type=int, nargs="+", default=[4, 128], help="token counts M to tune")
+    parser.add_argument("--write-table", action="store_true", help="store winners in the tuned table")
+    args = parser.parse_args(argv)
+
+    expected_type, kernel_module, factory = _BENCHMARKS[args.kernel]
+    if args.synthetic:
+        weight = synthetic_weight(*args.synthetic)
+    elif args.model and args.weight_name:
+        weight = load_gguf_weight(args.model, args.weight_name, expected_type)
+    else:
+        parser.error("give --model and --weight-name, or --synthetic N K")
+    module = importlib.import_module(kernel_module)
+    results = mini_benchmark(getattr(module, factory)(weight, tuple(args.tokens)))
+    if args.write_table:
+        from mambo_amd import _native
+        write_tuned_table(results, module.TUNED_PATH, _native.device_arch())
+    return results
+
+
+if __name__ == "__main__":
+    benchmark_main()

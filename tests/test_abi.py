@@ -1,0 +1,105 @@
+"""The C ABI library (no GPU): it loads, exports every entry point include/mambo_hip.h
+declares, and rejects bad arguments with the documented status codes before touching
+the device; the Python layer maps them to the reference's exception types."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import REPO
+
+HEADER = REPO / "include" / "mambo_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mambo_\w+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from mambo_amd import _native
+    lib = _native.lib()
+    names = declared_symbols()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in mambo_hip.h but not exported"
+    assert set(names) == set(_native.SIGNATURES), "ctypes declarations must match the header"
+    assert lib.mambo_abi_version() == 100
+    assert lib.mambo_build_arch() == b"gfx950"
+
+
+def test_status_codes_and_last_error():
+    from mambo_amd import _native
+    lib = _native.lib()
+    # K not divisible by 32 -> MAMBO_ERR_VALUE before any device work
+    rc = lib.mambo_quantize_mxfp8(None, 1, 4, 100, 100, None, 100, None, 4, None)
+    assert rc == _native.MAMBO_ERR_VALUE
+    assert b"K divisible by 32" in lib.mambo_last_error()
+    rc = lib.mambo_quantize_mxfp8(None, 7, 4, 64, 64, None, 64, None, 2, None)
+    assert rc == _native.MAMBO_ERR_VALUE and b"dtype" in lib.mambo_last_error()
+    with pytest.raises(ValueError, match="dtype"):
+        _native.check(rc)
+    rc = lib.mambo_iq3s_prepare(None, 4, 1, 110, 110, 1, None, None, None, None, None, None, None)
+    assert rc == _native.MAMBO_ERR_VALUE
+    assert lib.mambo_iq3s_packed_bytes(0, 3) == 0
+    assert lib.mambo_iq3s_packed_bytes(17, 3) == 2 * 3 * 1760
+    assert lib.mambo_iq3s_packed_bytes(4096, 16) == 4096 * 16 * 110  # byte-preserving
+
+
+def test_gemm_config_defaults_and_validation():
+    from mambo_amd import _native
+    lib = _native.lib()
+    cfg = _native.GemmConfig()
+    assert lib.mambo_gemm_default_config(1, 4096, 16, ctypes.byref(cfg)) == 0
+    assert cfg.kernel == _native.GEMM_STREAM and cfg.waves in (1, 2, 4, 8) and 1 <= cfg.split_k <= 16
+    big = _native.GemmConfig()
+    assert lib.mambo_gemm_default_config(1, 28672, 32, ctypes.byref(big)) == 0
+    assert big.split_k == 1  # enough row tiles to fill the GPU without splitting K
+    bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 3, "split_k": 1})
+    assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
+    bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 9})
+    assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
+    ok = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 8, "split_k": 4})
+    assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(ok)) == 0
+
+
+def test_codebook_exports_match_python_tables():
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import iq3_s_fp8_table, iq3_s_table
+    out = np.zeros(512, dtype=np.uint32)
+    assert _native.lib().mambo_iq3s_fp8_grid(out.ctypes.data) == 0
+    np.testing.assert_array_equal(out, iq3_s_fp8_table())
+    assert _native.lib().mambo_iq3s_grid(out.ctypes.data) == 0
+    np.testing.assert_array_equal(out, iq3_s_table())
+
+
+def test_python_api_validation_without_gpu():
+    import torch
+    from mambo_amd.kernels.iq3_s_fp8 import (launch_dequant_iq3_s, launch_iq3_s_fp8_matmul, m_bucket,
+                                             select_config)
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    with pytest.raises(ValueError):
+        launch_quantize_fp8(torch.zeros(4, 33))
+    with pytest.raises(ValueError):
+        launch_quantize_fp8(torch.zeros(4, 32, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        launch_quantize_fp8(torch.zeros(4, 64))  # not on a GPU
+    with pytest.raises(ValueError):
+        prepare_iq3_s_fields(torch.zeros(4, 2, 109, dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        prepare_iq3_s_fields(torch.zeros(0, 2, 110, dtype=torch.uint8))
+    with pytest.raises(TypeError):
+        launch_iq3_s_fp8_matmul(torch.zeros(1, 256, dtype=torch.uint8), torch.zeros(1, 8, dtype=torch.uint8),
+                                "not prepared")
+    with pytest.raises(TypeError):
+        launch_dequant_iq3_s(object())
+    with pytest.raises(RuntimeError, match="no tuned config"):
+        select_config(4, 4096, 4096, arch="gfx942")
+    assert select_config(4, 4096, 4096, arch="gfx950")["kernel"] == 1
+    assert [m_bucket(m) for m in (1, 2, 3, 4, 5, 16, 17, 2048)] == [1, 2, 4, 4, 8, 16, 32, 2048]

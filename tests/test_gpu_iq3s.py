@@ -1,0 +1,134 @@
+"""IQ3_S preparation and the standalone decoder on the GPU against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, all_codes_blocks, make_synthetic_iq3_s
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def step(msg: str) -> None:
+    print(f"[gpu] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("n_rows,blocks", [(7, 3), (1, 1), (33, 2)])
+def test_soa_fields_preserve_every_byte(gpu, n_rows, blocks):
+    """test_iq3_s_fp8.py:134-148."""
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    raw = make_synthetic_iq3_s(n_rows, blocks * 256, seed=0x50A)
+    step(f"prepare [{n_rows},{blocks},110]")
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    torch.cuda.synchronize()
+    reconstructed = np.empty_like(raw)
+    for field, start, end in ((fields.d, 0, 2), (fields.qs, 2, 66), (fields.qh, 66, 74),
+                              (fields.signs, 74, 106), (fields.scales, 106, 110)):
+        assert field.is_contiguous()
+        assert field.data_ptr() % field.element_size() == 0
+        data = field.cpu().view(torch.uint8).numpy().reshape(blocks, n_rows, end - start)
+        reconstructed[..., start:end] = data.transpose(1, 0, 2)
+    np.testing.assert_array_equal(reconstructed, raw)
+    assert sum(f.numel() * f.element_size() for f in (fields.d, fields.qs, fields.qh, fields.signs,
+                                                      fields.scales)) == raw.nbytes
+    # the private tile layout is a lossless permutation of the same bytes
+    np.testing.assert_array_equal(unpack_tiles(fields.packed.cpu().numpy(), n_rows, blocks), raw)
+
+
+def unpack_tiles(packed: np.ndarray, n: int, blocks: int) -> np.ndarray:
+    """Inverse of the 16-row x 1-block tile layout (mambo_amd/csrc/mambo_common.h)."""
+    tiles = (n + 15) // 16
+    p = packed.reshape(tiles, blocks, 1760)
+    raw = np.zeros((tiles, 16, blocks, 110), dtype=np.uint8)
+    for lane in range(64):
+        r, q = lane & 15, lane >> 4
+        words = p[:, :, 16 * lane:16 * lane + 16].copy().view("<u4").astype(np.uint64)
+        tail = p[:, :, 1024 + 2 * lane:1026 + 2 * lane].copy().view("<u2").astype(np.uint64)
+        w = [words[..., i] for i in range(4)] + [tail[..., 0], np.zeros_like(tail[..., 0])]
+        for i in range(16):
+            c = 16 * q + i
+            pos = 9 * i
+            wi, sh = pos // 32, pos % 32
+            val = ((w[wi] >> np.uint64(sh)) | (w[wi + 1] << np.uint64(32 - sh))) & np.uint64(0x1FF)
+            raw[:, r, :, 2 + c] = (val & np.uint64(0xFF)).astype(np.uint8)
+            raw[:, r, :, 66 + c // 8] |= ((val >> np.uint64(8)).astype(np.uint8) << np.uint8(c % 8))
+        for h in range(2):
+            t = p[:, :, 1152 + 8 * lane + 4 * h:1152 + 8 * lane + 4 * h + 4].copy().view("<u4")[..., 0]
+            sw = np.zeros_like(t)
+            for c in range(8):
+                for j in range(4):
+                    sw |= ((t >> np.uint32(c + 8 * j)) & np.uint32(1)) << np.uint32(4 * c + j)
+            raw[:, r, :, 74 + 4 * (2 * q + h):78 + 4 * (2 * q + h)] = sw[..., None].view(np.uint8).reshape(
+                tiles, blocks, 4)
+        raw[:, r, :, 106 + q] = p[:, :, 1664 + lane]
+        if q == 0:
+            raw[:, r, :, 0:2] = p[:, :, 1728 + 2 * r:1730 + 2 * r]
+    return raw.reshape(tiles * 16, blocks, 110)[:n]
+
+
+def test_packed_decode_all_codes_and_sign_nibbles(gpu):
+    """test_iq3_s_fp8.py:105-131: aligned, odd-address and strided sources all decode
+    exactly to +-grid magnitudes."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_dequant_iq3_s
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    from conftest import e4m3_values
+    raw, code, sign = all_codes_blocks()
+    expected = oracle.dequant_iq3s(raw)
+    aligned = torch.from_numpy(raw).to(gpu)
+    allocation = torch.empty(raw.size + 1, dtype=torch.uint8, device=gpu)
+    unaligned = allocation[1:].view(raw.shape)
+    unaligned.copy_(aligned)
+    strided_allocation = torch.empty((8, 16, 2 * 110), dtype=torch.uint8, device=gpu)
+    strided = strided_allocation[..., ::2]
+    strided.copy_(aligned)
+    vals = e4m3_values().astype(np.float32)
+    for name, source in (("aligned", aligned), ("unaligned", unaligned), ("strided", strided)):
+        step(f"prepare+dequant all codes ({name})")
+        fields = prepare_iq3_s_fields(source)
+        bits, scales = launch_dequant_iq3_s(fields, tile_n=4)
+        torch.cuda.synchronize()
+        actual = vals[bits.cpu().numpy()] * np.repeat(scales.cpu().numpy(), 32, axis=1)
+        np.testing.assert_array_equal(actual, expected)
+
+
+def test_decode_matches_oracle_and_golden(gpu):
+    from mambo_amd.kernels.iq3_s_fp8 import launch_dequant_iq3_s
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    g = np.load(GOLDEN / "decode_random.npz")
+    step("dequant golden [5,3,110]")
+    bits, scales = launch_dequant_iq3_s(prepare_iq3_s_fields(torch.from_numpy(g["raw"]).to(gpu)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits.cpu().numpy(), g["values"])
+    np.testing.assert_array_equal(scales.cpu().numpy(), g["scales"])
+    raw = make_synthetic_iq3_s(300, 12 * 256, seed=99)
+    step("dequant random [300,12,110]")
+    bits, scales = launch_dequant_iq3_s(prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu)))
+    torch.cuda.synchronize()
+    eb, es = oracle.dequant_iq3s_fp8(raw)
+    np.testing.assert_array_equal(bits.cpu().numpy(), eb)
+    np.testing.assert_array_equal(scales.cpu().numpy(), es)
+
+
+def test_pack_from_fields_matches_prepare(gpu):
+    from mambo_amd.utils.iq3_s_weight import IQ3SFields, ensure_packed, prepare_iq3_s_fields
+    raw = make_synthetic_iq3_s(45, 5 * 256, seed=3)
+    step("prepare + pack from SoA [45,5,110]")
+    f = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    g = IQ3SFields(f.d, f.qs, f.qh, f.signs, f.scales)
+    packed = ensure_packed(g)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, f.packed)
+
+
+def test_gpu_generator_matches_oracle_rows(gpu):
+    from mambo_amd import _native
+    blocks, rows = 32, 64
+    raw = torch.empty((rows, blocks, 110), dtype=torch.uint8, device=gpu)
+    step("synth iq3s rows 1000..1063")
+    _native.check(_native.lib().mambo_synth_iq3s(0, blocks, 1000, rows, raw.data_ptr(),
+                                                 _native.stream_handle(None)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(raw.cpu().numpy(), oracle.gen_iq3s(0, rows, blocks, row0=1000))

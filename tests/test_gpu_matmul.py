@@ -1,0 +1,162 @@
+"""Fused IQ3_S x MXFP8 projection on the GPU against the CPU oracle.
+
+Tolerances: rel-L2 <= 1e-3 against the float64-accumulated product of the decoded
+operands (the acceptance bar of the path), plus the reference test's elementwise
+rtol 5e-4 / atol 5e-3 (test_iq3_s_fp8.py:201)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, make_synthetic_iq3_s, rel_l2
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+RTOL, ATOL = 5e-4, 5e-3
+
+
+def step(msg: str) -> None:
+    print(f"[gpu] {msg}", flush=True)
+
+
+def check(out: np.ndarray, expected: np.ndarray, *, elementwise: bool = True) -> None:
+    assert out.shape == expected.shape and out.dtype == np.float32
+    err = rel_l2(out, expected)
+    assert err <= REL_L2, f"rel-L2 {err:.3e}"
+    if elementwise:
+        np.testing.assert_allclose(out, expected, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16, 17, 33, 128, 129])
+def test_synthetic_iq3_s_fp8_matmul_matches_oracle(gpu, m):
+    """test_iq3_s_fp8.py:178-210: N=7, K=768, reference block generator; also strided
+    activations (column stride 2, as the reference test passes them)."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n_rows, k = 7, 768
+    raw = make_synthetic_iq3_s(n_rows, k, seed=0x3F8)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    x = np.random.default_rng(20261016 + m).standard_normal((m, k)).astype(np.float32)
+    step(f"quantize + matmul M={m} N=7 K=768")
+    xq, xs = launch_quantize_fp8(torch.from_numpy(x).to(gpu))
+    out = launch_iq3_s_fp8_matmul(xq, xs, fields)
+    torch.cuda.synchronize()
+    expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw)
+    check(out.cpu().numpy(), expected)
+    strided_values = torch.empty((m, 2 * k), dtype=torch.uint8, device=gpu)
+    strided_values[:, ::2] = xq
+    strided_scales = torch.empty((m, 2 * k // 32), dtype=torch.uint8, device=gpu)
+    strided_scales[:, ::2] = xs
+    step(f"matmul strided activations M={m}")
+    out2 = launch_iq3_s_fp8_matmul(strided_values[:, ::2], strided_scales[:, ::2], fields)
+    torch.cuda.synchronize()
+    check(out2.cpu().numpy(), expected)
+
+
+def test_golden_matmul_small(gpu):
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    g = np.load(GOLDEN / "matmul_small.npz")
+    fields = prepare_iq3_s_fields(torch.from_numpy(g["raw"]).to(gpu))
+    step("matmul golden M=9 N=7 K=768")
+    out = launch_iq3_s_fp8_matmul(torch.from_numpy(g["x_values"]).to(gpu), torch.from_numpy(g["x_scales"]).to(gpu),
+                                  fields)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), g["out"])
+
+
+def test_every_search_space_config_agrees(gpu):
+    from mambo_amd.kernels.iq3_s_fp8 import gemm_search_space, launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n_rows, k = 100, 2048
+    raw = make_synthetic_iq3_s(n_rows, k, seed=17)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    for m in (1, 6, 16):
+        x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+        xv, xs = oracle.quantize_mxfp8(x)
+        expected = oracle.iq3s_fp8_matmul(xv, xs, raw)
+        xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+        for cfg in gemm_search_space(m, n_rows, k):
+            step(f"matmul M={m} N=100 K=2048 cfg={cfg}")
+            out = launch_iq3_s_fp8_matmul(xvg, xsg, fields, config=cfg)
+            torch.cuda.synchronize()
+            check(out.cpu().numpy(), expected)
+
+
+def test_output_row_stride_and_preallocated_out(gpu):
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    raw = make_synthetic_iq3_s(40, 1024, seed=21)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    x = np.random.default_rng(1).standard_normal((6, 1024)).astype(np.float32)
+    xv, xs = oracle.quantize_mxfp8(x)
+    expected = oracle.iq3s_fp8_matmul(xv, xs, raw)
+    big = torch.full((6, 64), 7.0, dtype=torch.float32, device=gpu)
+    for cfg in ({"waves": 4, "split_k": 1}, {"waves": 2, "split_k": 4}):
+        step(f"matmul into strided out cfg={cfg}")
+        launch_iq3_s_fp8_matmul(torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu), fields,
+                                config=cfg, out=big[:, 8:48])
+        torch.cuda.synchronize()
+        b = big.cpu().numpy()
+        check(b[:, 8:48], expected)
+        assert np.all(b[:, :8] == 7.0) and np.all(b[:, 48:] == 7.0)
+
+
+def _synth_weight(gpu, n: int, k: int, seed: int):
+    from mambo_amd import _native
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    raw = torch.empty((n, k // 256, 110), dtype=torch.uint8, device=gpu)
+    _native.check(_native.lib().mambo_synth_iq3s(seed, k // 256, 0, n, raw.data_ptr(), _native.stream_handle(None)))
+    return prepare_iq3_s_fields(raw, fields=False)
+
+
+def _synth_act(gpu, m: int, k: int, seed: int = 1):
+    from mambo_amd import _native
+    bits = torch.empty(m * k, dtype=torch.int16, device=gpu)
+    _native.check(_native.lib().mambo_synth_bf16(seed, 2, 0.0, 0, m * k, bits.data_ptr(), _native.stream_handle(None)))
+    return bits.view(torch.bfloat16).view(m, k)
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_llama3_8b_decode_shapes(gpu, n, k, m):
+    """Decode-shaped projections on the 8B shapes, weights from the counter-based
+    generator: full output for the smaller shapes, sampled rows for the larger."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    step(f"synth weight {n}x{k}")
+    fields = _synth_weight(gpu, n, k, seed=0)
+    step(f"quantize + matmul M={m} {n}x{k}")
+    xq, xs = launch_quantize_fp8(_synth_act(gpu, m, k))
+    out = launch_iq3_s_fp8_matmul(xq, xs, fields).cpu().numpy()
+    torch.cuda.synchronize()
+    rows = np.arange(n) if n * k <= 4096 * 4096 else np.concatenate(
+        [np.arange(256), np.random.default_rng(n).choice(n, 256, replace=False)])
+    raw = np.concatenate([oracle.gen_iq3s(0, 1, k // 256, row0=int(r)) for r in rows]) if len(rows) < n \
+        else oracle.gen_iq3s(0, n, k // 256)
+    expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
+    check(out[:, rows], expected, elementwise=False)
+    assert np.all(np.isfinite(out))
+
+
+@pytest.mark.parametrize("m", [1, 32])
+def test_llama3_70b_gate_shape_sampled(gpu, m):
+    """28672 x 8192 (gate/up), sampled output rows against the oracle."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    n, k = 28672, 8192
+    step(f"synth weight {n}x{k}")
+    fields = _synth_weight(gpu, n, k, seed=5)
+    step(f"quantize + matmul M={m} {n}x{k}")
+    xq, xs = launch_quantize_fp8(_synth_act(gpu, m, k, seed=9))
+    out = launch_iq3_s_fp8_matmul(xq, xs, fields).cpu().numpy()
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(1).choice(n, 192, replace=False))
+    raw = np.concatenate([oracle.gen_iq3s(5, 1, k // 256, row0=int(r)) for r in rows])
+    expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
+    check(out[:, rows], expected, elementwise=False)
