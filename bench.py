@@ -126,9 +126,12 @@ def run_gemm(args):
             o.fill_(float("nan"))
         graph.replay()
         torch.cuda.synchronize()
-        for (_, _, _, _, _, o) in launches:
-            if not torch.allclose(o, ref[id(o)], rtol=1e-5, atol=1e-6):
-                raise RuntimeError("graph replay differs from eager launch")
+        for (name, n, k, _, _, o) in launches:
+            r = ref[id(o)]
+            if not torch.allclose(o, r, rtol=1e-5, atol=1e-5):
+                diff = (o - r).abs().max().item()
+                raise RuntimeError(f"graph replay differs from eager launch ({name} {n}x{k}: max diff "
+                                   f"{diff}, nan {int(torch.isnan(o).sum())}, ref nan {int(torch.isnan(r).sum())})")
         replay = graph.replay
         log("captured the step in a HIP graph; replay matches eager")
 

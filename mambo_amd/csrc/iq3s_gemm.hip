@@ -12,8 +12,11 @@
 //
 // Per super-block each lane decodes 16 four-weight codes (groups 2q and 2q+1 of row
 // col, q = lane/16, col = lane%16) straight into the B operand of
-// V_MFMA_SCALE_F32_16X16X128_F8F6F4: lane l of B holds K chunk q (32 bytes) of column
-// col, so one lane's decoded group is exactly its B slice; nothing decoded touches HBM.
+// V_MFMA_SCALE_F32_16X16X128_F8F6F4: lane l of B holds 32 bytes of column col (K chunk
+// q: k in [16q, 16q+16) and [64+16q, 64+16q+16), byte t of lane l of A pairing with
+// byte t of lane l' of B for l >> 4 == l' >> 4), so one lane's decoded group is exactly
+// its B slice; nothing decoded touches HBM. Layout measured on gfx950 with one-hot
+// operands.
 //   code address: 2 VALU (funnel shift + mask of the 9-bit index stream)
 //   magnitude:    1 LDS read of the E4M3-encoded grid word
 //   signs:        2 VALU (rotate the bit-transposed sign word, bit-field insert)
@@ -165,15 +168,23 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     const int col = lane & 15, q = lane >> 4;
     const bool a_lane = (col >> 2) == q;
 
+    // A operand (activations). Data: lane l holds row i = l & 15 = 4*g' + m' in K chunk
+    // l >> 4; it is non-zero only when the chunk is g' (block-diagonal). Scales: the
+    // E8M0 scale of (row i, K block kb) comes from lane i + 16*kb, and a lane's 32 bytes
+    // span two K blocks (bytes 0-15 in block q/2, bytes 16-31 in block 2 + q/2), so the
+    // lanes holding row i's scales are those with kb & 1 == g' >> 1.
+    const int g_row = (lane & 15) >> 2;
+    const bool s_lane = ((lane >> 4) & 1) == (g_row >> 1);
     ALane al[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t m = m0 + 4 * u + (lane & 3);
         const bool on = a_lane && m < M;
+        const bool son = s_lane && m < M;
         al[u].x = on ? xv + m * ldxv + 64 * q : g_zero_chunk;
-        al[u].s = on ? xs + m * ldxs + 2 * q : g_unit_scales;
+        al[u].s = son ? xs + m * ldxs + 2 * g_row : g_unit_scales;
         al[u].xstep = on ? 256 : 0;
-        al[u].sstep = on ? 8 : 0;
+        al[u].sstep = son ? 8 : 0;
     }
 
     float acc[U][4];

@@ -15,8 +15,10 @@
 namespace {
 
 // E4M3 rounding path of the quantizer: hardware v_cvt_pk_fp8_f32 (true) or the integer
-// restatement e4m3_rne_sw (false).
-constexpr bool kQuantHwCvt = false;
+// restatement e4m3_rne_sw (false). The two agree on every f32 with |x| <= 464 (checked
+// on gfx950 over all 2^31 such bit patterns with both signs); the quantizer only feeds
+// |x * 2^-e| <= 448.
+constexpr bool kQuantHwCvt = true;
 
 template <bool kBf16>
 __device__ __forceinline__ void load8(const void *__restrict__ x, int64_t off, float v[8])

@@ -160,3 +160,40 @@ def test_llama3_70b_gate_shape_sampled(gpu, m):
     raw = np.concatenate([oracle.gen_iq3s(5, 1, k // 256, row0=int(r)) for r in rows])
     expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
     check(out[:, rows], expected, elementwise=False)
+
+
+def test_graph_capture_replays_match_eager(gpu):
+    """Split-K launches (zero-fill kernel + atomics) captured in a HIP graph: every replay,
+    with eager work between replays, matches the eager result."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    fields = [_synth_weight(gpu, 1024, 4096, seed=s) for s in (11, 12)]
+    xq, xs = launch_quantize_fp8(_synth_act(gpu, 4, 4096))
+    outs = [torch.empty((4, 1024), dtype=torch.float32, device=gpu) for _ in fields]
+    cfgs = [{"waves": 4, "split_k": 4}, {"waves": 2, "split_k": 1}]
+
+    def step_fn():
+        for f, o, c in zip(fields, outs, cfgs):
+            launch_iq3_s_fp8_matmul(xq, xs, f, config=c, out=o)
+
+    step("eager reference")
+    step_fn()
+    torch.cuda.synchronize()
+    ref = [o.clone() for o in outs]
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    step("capture")
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            step_fn()
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        step(f"replay {rep}")
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            torch.testing.assert_close(o, r, rtol=1e-5, atol=1e-5)
+        _ = (xq.float().sum()).item()  # eager work between replays
