@@ -13,7 +13,7 @@ value = algorithmic bytes per step / step time, with
                          + 4*M*N (f32 output)
 roofline: HBM (8 TB/s) for the weight stream. cpu_baseline: the oracle's restatement of
 the reference CPU path (ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot) on
-BASELINE config 1 (N=K=4096, M=8), timed on this host.
+its CPU case, one IQ3_S linear N=K=4096 with M=8, timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant]
 """
@@ -159,7 +159,7 @@ def run_gemm(args):
 
 
 def cpu_baseline(seconds: float) -> dict:
-    """Oracle restatement of the reference CPU path on config 1: one IQ3_S linear
+    """Oracle restatement of the reference CPU path on its CPU case: one IQ3_S linear
     N=K=4096 (seed-0 counter-based blocks), M=8 bf16 ~N(0,1) activations quantized to
     MXFP8, IQ3_S to_float + float64-accumulated dot per output (all host cores)."""
     import numpy as np
@@ -178,7 +178,7 @@ def cpu_baseline(seconds: float) -> dict:
     per = (time.perf_counter() - t0) / iters
     gbs = proj_bytes(m, n, k) / per / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"BASELINE config 1: N=K=4096, M=8, {iters} runs in {per * iters:.1f} s "
+            "sample": f"one IQ3_S linear N=K=4096, M=8 (the reference CPU case): {iters} runs in {per * iters:.1f} s "
                       f"({per * 1e3:.1f} ms each) of the oracle's to_float + f64-dot restatement "
                       f"of ggml_reference.cpp:495-523 on {threads} threads"}
 

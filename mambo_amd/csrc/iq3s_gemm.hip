@@ -39,6 +39,15 @@ __constant__ GridTables c_grid = kGridTables;
 __device__ __align__(16) uint8_t g_zero_chunk[64] = {};
 __device__ uint8_t g_unit_scales[2] = {127, 127};
 
+// Super-blocks in flight per wave (register ring depth).
+#ifndef MAMBO_STREAM_DEPTH
+#define MAMBO_STREAM_DEPTH 2
+#endif
+constexpr int kDepth = MAMBO_STREAM_DEPTH;
+#ifndef MAMBO_SCHED_FENCE
+#define MAMBO_SCHED_FENCE 1
+#endif
+
 
 struct WTile {
     uint4 ia;     // idx stream bits 0..127
@@ -99,13 +108,17 @@ struct ATile {
     uint8_t s[U][2];
 };
 
-// Activation slices of one super-block. Lanes outside the block-diagonal (and rows
-// past M) read a zero buffer with a zero stride, so every load is unconditional.
+// Activation operand of one lane. Data: lane l holds row i = l & 15 = 4*g' + m' in K
+// chunk l >> 4 and is non-zero only when that chunk is g' (block-diagonal). Scales: the
+// E8M0 scale of (row i, K block kb) comes from lane i + 16*kb, and a lane's 32 bytes span
+// two K blocks (bytes 0-15 in block q/2, bytes 16-31 in block 2 + q/2), so the lanes
+// holding row i's scales are those with kb & 1 == g' >> 1. Lanes outside the diagonal
+// (and rows past M) point at a zero chunk / unit scales with a zero stride.
 struct ALane {
     const uint8_t *x;  // activation bytes of this lane's chunk, block 0
     const uint8_t *s;  // E8M0 scale of this lane's chunk, block 0
-    int64_t xstep;     // 256 or 0
-    int64_t sstep;     // 8 or 0
+    int xstep;         // 256 or 0
+    int sstep;         // 8 or 0
 };
 
 template <int U>
@@ -113,8 +126,8 @@ __device__ __forceinline__ void load_a(ATile<U> &at, const ALane (&al)[U], int b
 {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint8_t *xp = al[u].x + (int64_t)b * al[u].xstep;
-        const uint8_t *sp = al[u].s + (int64_t)b * al[u].sstep;
+        const uint8_t *xp = al[u].x + b * al[u].xstep;
+        const uint8_t *sp = al[u].s + b * al[u].sstep;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint4 *p = reinterpret_cast<const uint4 *>(xp + 32 * h);
@@ -126,15 +139,17 @@ __device__ __forceinline__ void load_a(ATile<U> &at, const ALane (&al)[U], int b
 }
 
 template <int U>
-__device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at, const uint8_t *lut, float (&acc)[U][4])
+__device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at, const uint8_t *lut, float (&acc)[U][4],
+                                              bool valid)
 {
     const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
     const float d = half_bits_to_float((uint16_t)w.dh);
     const v8i b0 = decode_group<0>(s, w.sg.x, lut, std::make_integer_sequence<int, 8>{});
     const v8i b1 = decode_group<1>(s, w.sg.y, lut, std::make_integer_sequence<int, 8>{});
     const uint32_t sc = w.sc;
-    const float f0 = d * (float)(1u + 2u * (sc & 15u));
-    const float f1 = d * (float)(1u + 2u * (sc >> 4));
+    // A block past the wave's range (a duplicate of its last block) contributes nothing.
+    const float f0 = valid ? d * (float)(1u + 2u * (sc & 15u)) : 0.0f;
+    const float f1 = valid ? d * (float)(1u + 2u * (sc >> 4)) : 0.0f;
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -146,43 +161,90 @@ __device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at
     }
 }
 
-template <int U, int W>
+// Dynamic LDS of the stream kernel: codebook (2 KiB), cross-wave partial sums of one
+// 4-row sub-tile [W][4][64] f32, a zero chunk + unit scales for lanes off the block diagonal, and -
+// when kLdsAct - the workgroup's activation rows [rows][K] and scales [rows][K/32].
+struct StreamLds {
+    int red, zero, x, xs, total;
+};
+
+__host__ __device__ inline StreamLds stream_lds(int U, int W, int rows, int K, bool lds_act)
+{
+    StreamLds l;
+    l.red = 2048;
+    l.zero = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
+    (void)U;
+    l.x = l.zero + 80;
+    l.xs = l.x + (lds_act ? rows * K : 0);
+    l.total = l.xs + (lds_act ? rows * (K / 32) : 0);
+    return l;
+}
+
+template <int U, int W, bool kLdsAct>
 __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                              const uint8_t *__restrict__ packed, int64_t N, int B,
                                                              int bps, float *__restrict__ out, int64_t ldo, int atomic)
 {
-    __shared__ uint32_t lut_words[512];
-    __shared__ float red[W][U * 4][64];
+    extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: scalar loop control
-    for (int i = tid; i < 512; i += W * 64)
-        lut_words[i] = c_grid.fp8[i];
-    __syncthreads();
-    const uint8_t *lut = reinterpret_cast<const uint8_t *>(lut_words);
-
+    const int K = B * 256;
+    const int64_t m0 = (int64_t)blockIdx.z * 16;
+    const int rows = (int)min<int64_t>(U * 4, M - m0);
+    const StreamLds L = stream_lds(U, W, rows, K, kLdsAct);
     const int64_t t = blockIdx.x;
     const int b_begin = blockIdx.y * bps;
     const int b_end = min(B, b_begin + bps);
-    const int64_t m0 = (int64_t)blockIdx.z * 16;
     const int col = lane & 15, q = lane >> 4;
-    const bool a_lane = (col >> 2) == q;
+    const uint8_t *wt = packed + t * (int64_t)B * kTileBytes;
+    // Blocks of this wave: first, first + W, ... (count is wave-uniform).
+    const int first = b_begin + wave;
+    const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
+    const int last = first + (count - 1) * W;
+    WTile wr[kDepth];
+    const uint8_t *lut = smem;
+    {
+        const int nt = W * 64;
+        uint32_t *lw = reinterpret_cast<uint32_t *>(smem);
+        for (int i = tid; i < 512; i += nt)
+            lw[i] = c_grid.fp8[i];
+        if (tid < 20)
+            reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 16 ? 0u : 0x7F7F7F7Fu;
+        if constexpr (kLdsAct) {
+            // activation rows m0 .. m0+rows-1: K is a multiple of 256, so 16-byte chunks
+            // never straddle rows
+            const int nx = rows * K / 16;
+            for (int c = tid; c < nx; c += nt) {
+                const int r = c * 16 / K;
+                *reinterpret_cast<uint4 *>(smem + L.x + c * 16) =
+                    *reinterpret_cast<const uint4 *>(xv + (m0 + r) * ldxv + (c * 16 - r * K));
+            }
+            const int ns = rows * (K / 32);
+            for (int i = tid; i < ns; i += nt) {
+                const int r = i / (K / 32);
+                smem[L.xs + i] = xs[(m0 + r) * ldxs + (i - r * (K / 32))];
+            }
+        }
+    }
+    __syncthreads();
 
-    // A operand (activations). Data: lane l holds row i = l & 15 = 4*g' + m' in K chunk
-    // l >> 4; it is non-zero only when the chunk is g' (block-diagonal). Scales: the
-    // E8M0 scale of (row i, K block kb) comes from lane i + 16*kb, and a lane's 32 bytes
-    // span two K blocks (bytes 0-15 in block q/2, bytes 16-31 in block 2 + q/2), so the
-    // lanes holding row i's scales are those with kb & 1 == g' >> 1.
-    const int g_row = (lane & 15) >> 2;
+    const bool a_lane = (col >> 2) == q;
+    const int g_row = col >> 2;
     const bool s_lane = ((lane >> 4) & 1) == (g_row >> 1);
     ALane al[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t m = m0 + 4 * u + (lane & 3);
-        const bool on = a_lane && m < M;
-        const bool son = s_lane && m < M;
-        al[u].x = on ? xv + m * ldxv + 64 * q : g_zero_chunk;
-        al[u].s = son ? xs + m * ldxs + 2 * g_row : g_unit_scales;
+        const int r = 4 * u + (lane & 3); // row within the chunk
+        const bool on = a_lane && r < rows;
+        const bool son = s_lane && r < rows;
+        if constexpr (kLdsAct) {
+            al[u].x = on ? smem + L.x + r * K + 64 * q : smem + L.zero;
+            al[u].s = son ? smem + L.xs + r * (K / 32) + 2 * g_row : smem + L.zero + 64;
+        } else {
+            al[u].x = on ? xv + (m0 + r) * ldxv + 64 * q : g_zero_chunk;
+            al[u].s = son ? xs + (m0 + r) * ldxs + 2 * g_row : g_unit_scales;
+        }
         al[u].xstep = on ? 256 : 0;
         al[u].sstep = son ? 8 : 0;
     }
@@ -194,55 +256,101 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
         for (int r = 0; r < 4; ++r)
             acc[u][r] = 0.0f;
 
-    const uint8_t *wt = packed + t * (int64_t)B * kTileBytes;
-    // Blocks of this wave: b_begin + wave, + W, ... (count is wave-uniform).
-    const int first = b_begin + wave;
-    const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
+    // A ring of kDepth register sets with fixed slots (the loop body is unrolled kDepth
+    // times): block i is decoded while blocks i+1 .. i+kDepth-1 are in flight. Prefetch
+    // addresses are clamped to the wave's last block and blocks past the end get a zero
+    // group scale, so the body has no branches and every load stays ahead of its use.
+    // Activations staged in LDS are read at decode time; otherwise they ride in the ring
+    // with the weights.
     if (count > 0) {
-        // Two register sets used in turn; each loop trip decodes exactly two blocks while
-        // the next one is in flight. The prefetch after the last pair re-reads a block
-        // of this wave (a cache hit) so every load is unconditional and stays ahead of
-        // its use. An odd final block is decoded after the loop.
-        const int last = first + (count - 1) * W;
-        int b = first;
-        WTile w0 = load_w(wt + (int64_t)b * kTileBytes, lane, col), w1;
-        ATile<U> a0, a1;
-        load_a<U>(a0, al, b);
-        for (int pair = 0; pair < count / 2; ++pair) {
-            w1 = load_w(wt + (int64_t)(b + W) * kTileBytes, lane, col);
-            load_a<U>(a1, al, b + W);
-            compute_block<U>(w0, a0, lut, acc);
-            const int b2 = min(b + 2 * W, last);
-            w0 = load_w(wt + (int64_t)b2 * kTileBytes, lane, col);
-            load_a<U>(a0, al, b2);
-            compute_block<U>(w1, a1, lut, acc);
-            b += 2 * W;
+#pragma unroll
+        for (int j = 0; j < kDepth - 1; ++j)
+            wr[j] = load_w(wt + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
+        ATile<U> ar[kLdsAct ? 1 : kDepth];
+        if constexpr (!kLdsAct) {
+#pragma unroll
+            for (int j = 0; j < kDepth - 1; ++j)
+                load_a<U>(ar[j], al, min(first + j * W, last));
         }
-        if (count & 1)
-            compute_block<U>(w0, a0, lut, acc);
+        for (int i0 = 0; i0 < count; i0 += kDepth) {
+#pragma unroll
+            for (int j = 0; j < kDepth; ++j) {
+                const int i = i0 + j;
+                const int slot = (j + kDepth - 1) % kDepth;
+                const int bp = min(first + (i + kDepth - 1) * W, last);
+                wr[slot] = load_w(wt + (int64_t)bp * kTileBytes, lane, col);
+                if constexpr (!kLdsAct)
+                    load_a<U>(ar[slot], al, bp);
+                // keep the prefetch issued before the decode of block i (scheduler fence)
+                if constexpr (MAMBO_SCHED_FENCE)
+                    __builtin_amdgcn_sched_barrier(0);
+                if constexpr (kLdsAct) {
+                    load_a<U>(ar[0], al, min(first + i * W, last));
+                    compute_block<U>(wr[j], ar[0], lut, acc, i < count);
+                } else {
+                    compute_block<U>(wr[j], ar[j], lut, acc, i < count);
+                }
+                if constexpr (MAMBO_SCHED_FENCE)
+                    __builtin_amdgcn_sched_barrier(0);
+            }
+        }
     }
 
+    if constexpr (W == 1) {
+        // sum the four K chunks (lanes col, col+16, col+32, col+48) within the wave
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            red[wave][u * 4 + r][lane] = acc[u][r];
-    __syncthreads();
-    for (int i = tid; i < U * 4 * 16; i += W * 64) {
-        const int ur = i >> 4, c = i & 15;
-        float v = 0.0f;
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[u][r];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                acc[u][r] = v;
+            }
+        if (lane < 16) {
+            const int64_t n = t * kTileRows + lane;
 #pragma unroll
-        for (int w = 0; w < W; ++w)
+            for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int qq = 0; qq < 4; ++qq)
-                v += red[w][ur][qq * 16 + c];
-        const int64_t m = m0 + ur, n = t * kTileRows + c;
-        if (m < M && n < N) {
-            float *o = out + m * ldo + n;
-            if (atomic)
-                atomicAdd(o, v);
-            else
-                *o = v;
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t m = m0 + 4 * u + r;
+                    if (m < M && n < N) {
+                        float *o = out + m * ldo + n;
+                        if (atomic)
+                            atomicAdd(o, acc[u][r]);
+                        else
+                            *o = acc[u][r];
+                    }
+                }
+        }
+    } else {
+        // cross-wave sum through LDS, one 4-row sub-tile at a time
+        float *red = reinterpret_cast<float *>(smem + L.red);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (u > 0)
+                __syncthreads();
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[(wave * 4 + r) * 64 + lane] = acc[u][r];
+            __syncthreads();
+            for (int i = tid; i < 4 * 16; i += W * 64) {
+                const int r = i >> 4, c = i & 15;
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < W; ++w)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq)
+                        v += red[(w * 4 + r) * 64 + qq * 16 + c];
+                const int64_t m = m0 + 4 * u + r, n = t * kTileRows + c;
+                if (m < M && n < N) {
+                    float *o = out + m * ldo + n;
+                    if (atomic)
+                        atomicAdd(o, v);
+                    else
+                        *o = v;
+                }
+            }
         }
     }
 }
@@ -255,30 +363,65 @@ __global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t 
     (void)rows;
 }
 
-template <int U, int W>
-void launch_stream_uw(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
-                      int64_t M, const uint8_t *packed, int64_t N, int B, int bps, float *out, int64_t ldo, int atomic)
+template <int U, int W, bool kLdsAct>
+void launch_stream_uwa(dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
+                       int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B, int bps, float *out,
+                       int64_t ldo, int atomic)
 {
-    hipLaunchKernelGGL((gemm_stream_kernel<U, W>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs, ldxs, M, packed, N, B,
-                       bps, out, ldo, atomic);
+    hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
+                       packed, N, B, bps, out, ldo, atomic);
 }
 
-template <int U>
-int launch_stream_u(int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
-                    int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B, int bps, float *out, int64_t ldo,
-                    int atomic)
+template <int U, int W>
+void launch_stream_uw(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                      const uint8_t *xs, int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B, int bps,
+                      float *out, int64_t ldo, int atomic)
 {
+    if (lds_act)
+        launch_stream_uwa<U, W, true>(grid, lds, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic);
+    else
+        launch_stream_uwa<U, W, false>(grid, lds, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic);
+}
+
+// Waves per workgroup the stream kernel is built for.
+constexpr int kStreamWaves[] = {1, 2, 4, 6, 8, 12, 16};
+
+template <int U>
+int launch_stream_u(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
+                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B,
+                    int bps, float *out, int64_t ldo, int atomic)
+{
+#define MAMBO_W(WV)                                                                                                \
+    case WV:                                                                                                       \
+        launch_stream_uw<U, WV>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo,    \
+                                atomic);                                                                           \
+        break;
     switch (waves) {
-    case 1: launch_stream_uw<U, 1>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
-    case 2: launch_stream_uw<U, 2>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
-    case 4: launch_stream_uw<U, 4>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
-    case 8: launch_stream_uw<U, 8>(grid, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic); break;
-    default: return mambo_fail(MAMBO_ERR_VALUE, "waves must be 1, 2, 4 or 8 (got %d)", waves);
+        MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
+    default:
+        return mambo_fail(MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16 (got %d)", waves);
     }
+#undef MAMBO_W
     return MAMBO_OK;
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Waves the default configuration aims for: about two rounds of 4 resident waves per
+// SIMD (4 SIMDs x 256 CUs).
+constexpr int64_t kTargetWaves = 8192;
+// Below this many waves the default config splits K.
+constexpr int64_t kMinWaves = 512;
+// Activations are staged in LDS when the workgroup's rows take at most this much.
+constexpr int kMaxLdsAct = 40 * 1024;
+
+bool valid_waves(int w)
+{
+    for (int v : kStreamWaves)
+        if (v == w)
+            return true;
+    return false;
+}
 
 } // namespace
 
@@ -288,13 +431,24 @@ extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, m
     MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
     mambo_gemm_config c = {};
     c.kernel = MAMBO_GEMM_STREAM;
-    c.waves = 4;
-    const int64_t tiles = cdiv(n, kTileRows) * cdiv(m, 16);
-    // Aim for >= 2 workgroups of 4 waves per CU (256 CUs) with >= 2 blocks per wave.
-    int64_t split = cdiv(512, tiles);
-    const int64_t max_split = std::max<int64_t>(1, blocks / (2 * c.waves));
-    split = std::min<int64_t>(std::max<int64_t>(split, 1), max_split);
-    c.split_k = (int32_t)split;
+    const int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
+    // Waves per workgroup: the largest power of two up to 8 (16 for grids of at most 2K
+    // waves) that divides the K blocks evenly, keeps at least two blocks per wave and at
+    // most about two residency rounds of waves in the grid (measured on gfx950: deeper
+    // oversubscription and uneven splits both lose). K is split only when even that
+    // leaves the chip mostly idle: a split costs a zero fill and atomics, which lose to
+    // wider workgroups down to ~1K waves.
+    int waves = 1;
+    for (int w : {2, 4, 8, 16})
+        if (units * w <= (w < 16 ? kTargetWaves : kTargetWaves / 4) && blocks % w == 0 && blocks / w >= 2)
+            waves = w;
+    int64_t split = 1;
+    if (units * waves < kMinWaves) {
+        const int64_t per_split_waves = units * waves;
+        split = std::min<int64_t>(cdiv(kMinWaves, per_split_waves), std::max<int64_t>(1, blocks / (2 * waves)));
+    }
+    c.waves = waves;
+    c.split_k = (int32_t)std::max<int64_t>(split, 1);
     *out = c;
     return MAMBO_OK;
 }
@@ -304,8 +458,7 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
     MAMBO_REQUIRE(cfg != nullptr, MAMBO_ERR_VALUE, "cfg must not be NULL");
     MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
     MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM, MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
-    MAMBO_REQUIRE(cfg->waves == 1 || cfg->waves == 2 || cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE,
-                  "waves must be 1, 2, 4 or 8");
+    MAMBO_REQUIRE(valid_waves(cfg->waves), MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16");
     MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                   "split_k must be in [1, K/256]");
     return MAMBO_OK;
@@ -318,7 +471,7 @@ extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint
     MAMBO_REQUIRE(xv && xs && packed && out, MAMBO_ERR_VALUE, "null pointer");
     MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive (M=%lld N=%lld B=%lld)",
                   (long long)m, (long long)n, (long long)blocks);
-    MAMBO_REQUIRE(blocks <= 0x7FFFFFFF / 8, MAMBO_ERR_VALUE, "K too large");
+    MAMBO_REQUIRE(blocks <= (1 << 20), MAMBO_ERR_VALUE, "K too large");
     const int64_t k = blocks * 256;
     MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32 && ldo >= n, MAMBO_ERR_VALUE, "row strides must cover the row");
     MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
@@ -352,20 +505,30 @@ extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint
     const int splits = (int)cdiv(blocks, bps);
     const int atomic = splits > 1;
     if (atomic) {
-        dim3 zg((unsigned)std::min<int64_t>(cdiv(n, 256), 1024), (unsigned)m);
         MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
+        dim3 zg((unsigned)std::min<int64_t>(cdiv(n, 256), 1024), (unsigned)m);
         hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, out, m, n, ldo);
         rc = mambo_check_launch("zero_rows");
         if (rc)
             return rc;
     }
-    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
     const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
+    const int rows = (int)std::min<int64_t>(16, m); // rows of the largest M chunk
+    // Stage the activations in LDS when they are small enough; otherwise read them from
+    // global memory (L2) in the weight ring.
+    bool lds_act = (int64_t)rows * k * 33 / 32 <= kMaxLdsAct;
+    if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > 64 * 1024)
+        lds_act = false;
+    const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
+    MAMBO_REQUIRE(L.total <= 64 * 1024, MAMBO_ERR_VALUE,
+                  "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
+                  c.waves, (long long)m);
+    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
     switch (U) {
-    case 1: rc = launch_stream_u<1>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
-    case 2: rc = launch_stream_u<2>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
-    case 3: rc = launch_stream_u<3>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
-    default: rc = launch_stream_u<4>(c.waves, grid, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    case 1: rc = launch_stream_u<1>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    case 2: rc = launch_stream_u<2>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    case 3: rc = launch_stream_u<3>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    default: rc = launch_stream_u<4>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
     }
     if (rc)
         return rc;

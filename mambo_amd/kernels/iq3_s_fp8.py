@@ -42,13 +42,14 @@ IQ3_S_SCALE_VALUES = 32
 _IQ3_TABLES: dict[int, torch.Tensor] = {}
 
 # Launch configurations per architecture, selected by token count as in the reference
-# (iq3_s_fp8.py:49-60). Fields follow mambo_gemm_config; 0 = library default for the
-# shape. Per-shape autotuned entries (tuned_gfx950.json, written by
+# (iq3_s_fp8.py:49-60). Fields follow mambo_gemm_config; 0 = the library's per-shape
+# default (waves sized so the whole grid is resident in one round, K split only for
+# small N). Per-shape autotuned entries (tuned_gfx950.json, written by
 # mambo_amd.utils.kernel_benchmark) take precedence.
 BEST_CONFIGS = {
     "gfx950": {
-        "medium": {"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 0},
-        "large": {"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 0},
+        "medium": {"kernel": _native.GEMM_STREAM, "waves": 0, "split_k": 0},
+        "large": {"kernel": _native.GEMM_STREAM, "waves": 0, "split_k": 0},
     },
 }
 LARGE_TOKEN_THRESHOLD = 32
@@ -190,10 +191,13 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
     search spaces of iq3_s_fp8.py:416-459): waves per workgroup x K split."""
     blocks = k // IQ3_S_BLOCK_VALUES
+    u = min(4, -(-m // 4))
     space = []
-    for waves in (1, 2, 4, 8):
-        for split in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
-            if split <= blocks and (blocks + split - 1) // split >= 1:
+    for waves in (1, 2, 4, 6, 8, 12, 16):
+        if waves * u > 32 or waves > blocks:
+            continue
+        for split in (1, 2, 4, 8):
+            if split <= blocks // waves:
                 space.append({"kernel": _native.GEMM_STREAM, "waves": waves, "split_k": split})
     return space
 

@@ -56,11 +56,15 @@ def test_gemm_config_defaults_and_validation():
     lib = _native.lib()
     cfg = _native.GemmConfig()
     assert lib.mambo_gemm_default_config(1, 4096, 16, ctypes.byref(cfg)) == 0
-    assert cfg.kernel == _native.GEMM_STREAM and cfg.waves in (1, 2, 4, 8) and 1 <= cfg.split_k <= 16
-    big = _native.GemmConfig()
-    assert lib.mambo_gemm_default_config(1, 28672, 32, ctypes.byref(big)) == 0
-    assert big.split_k == 1  # enough row tiles to fill the GPU without splitting K
-    bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 3, "split_k": 1})
+    assert cfg.kernel == _native.GEMM_STREAM and cfg.waves in (1, 2, 4, 6, 8, 12, 16) and 1 <= cfg.split_k <= 16
+    # about two residency rounds of waves, power-of-two waves dividing the blocks evenly,
+    # 16 waves only for small grids, K split only below 512 waves
+    for n, blocks, waves, split in ((28672, 32, 4, 1), (8192, 32, 8, 1), (8192, 112, 8, 1), (10240, 32, 8, 1),
+                                    (57344, 32, 2, 1), (1024, 32, 16, 1), (1024, 16, 8, 1), (64, 64, 16, 2)):
+        big = _native.GemmConfig()
+        assert lib.mambo_gemm_default_config(1, n, blocks, ctypes.byref(big)) == 0
+        assert (big.waves, big.split_k) == (waves, split), (n, blocks, big.as_dict())
+    bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 5, "split_k": 1})
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
     bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 9})
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
