@@ -15,7 +15,7 @@ roofline: HBM (8 TB/s) for the weight stream. cpu_baseline: the oracle's restate
 the reference CPU path (ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot) on
 its CPU case, one IQ3_S linear N=K=4096 with M=8, timed on this host.
 
-    python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant]
+    python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant|copy]
 """
 
 from __future__ import annotations
@@ -213,13 +213,56 @@ def run_quant(args):
             "per_launch_bytes": nbytes, "per_launch_us": ms * 1e3}
 
 
+COPY_BYTES = 1 << 30
+
+
+def run_copy(args):
+    """Plain copy of COPY_BYTES with mambo_copy_bytes: the calibration workload for the
+    HBM byte counters (every byte read once and written once)."""
+    import torch
+    from mambo_amd import _native
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+
+    def launch():
+        _native.check(_native.lib().mambo_copy_bytes(src.data_ptr(), dst.data_ptr(), COPY_BYTES,
+                                                     _native.stream_handle(None)), "copy")
+
+    for _ in range(args.warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        launch()
+    stop.record()
+    torch.cuda.synchronize()
+    if not bool((dst == 1).all()):
+        raise RuntimeError("copy kernel produced wrong bytes")
+    ms = start.elapsed_time(stop) / args.steps
+    nbytes = 2 * COPY_BYTES
+    return {"ms": ms, "value": nbytes / (ms * 1e-3) / 1e9, "step_bytes": nbytes, "launches": 1,
+            "per_launch_bytes": nbytes, "per_launch_us": ms * 1e3}
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel for `workload`, from the committed
+    counter summaries (profiles/traffic_*.json), or None when none matches."""
+    for path in sorted((REPO / "profiles").glob("traffic_*.json")):
+        rec = json.loads(path.read_text())
+        if rec.get("workload") == workload:
+            return round(rec["traffic_bytes_per_launch"])
+    return None
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--m", type=int, default=1, help="tokens per projection")
-    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant"], default="llama70b")
+    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy"], default="llama70b")
     p.add_argument("--layers", type=int, default=80, help="llama70b: layers in the sweep")
     p.add_argument("--copies", type=int, default=48, help="llama8b: distinct weight copies per shape")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -237,7 +280,12 @@ def main(argv=None) -> int:
     _native.lib()
     log(f"device {torch.cuda.get_device_name(0)} ({_native.device_arch()})")
 
-    if args.workload == "quant":
+    if args.workload == "copy":
+        r = run_copy(args)
+        metric = "plain device copy GB/s (HBM counter calibration)"
+        workload = f"copy {COPY_BYTES} bytes"
+        config = {"workload": workload}
+    elif args.workload == "quant":
         r = run_quant(args)
         metric = "MXFP8 activation quantizer GB/s (bf16 [4096,4096] -> E4M3 + E8M0)"
         workload = "mxfp8 quantize bf16 [4096,4096], 0.1% x100 outliers, 8 rotated inputs"
@@ -268,7 +316,7 @@ def main(argv=None) -> int:
         "data": "synthetic (counter-based IQ3_S blocks, bf16 ~N(0,1) activations)",
         "config": config,
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
                      "algorithmic_bytes_per_launch": round(r["per_launch_bytes"]),
                      "avg_launch_us": round(r["per_launch_us"], 3)},
     }

@@ -156,6 +156,12 @@ int mambo_e4m3_convert(const float *in, int64_t n, uint8_t *out_sw, uint8_t *out
  * a HIP graph). */
 int mambo_fill_f32(float *ptr, int64_t n, float value, mambo_stream_t stream);
 
+/* Diagnostic: copy `bytes` (a multiple of 16, both pointers 16-byte aligned) from src to
+ * dst with 16-byte vector loads and stores, each byte read and written exactly once. A
+ * plain stream of known size, used to calibrate the HBM byte counters (FETCH_SIZE,
+ * WRITE_SIZE) that the kernels' traffic figures are scaled by. */
+int mambo_copy_bytes(const void *src, void *dst, int64_t bytes, mambo_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

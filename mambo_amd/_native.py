@@ -78,6 +78,7 @@ SIGNATURES = {
     "mambo_synth_bf16": (_i32, [_u64, _u64, ctypes.c_double, _i64, _i64, _vp, _vp]),
     "mambo_e4m3_convert": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "mambo_fill_f32": (_i32, [_vp, _i64, ctypes.c_float, _vp]),
+    "mambo_copy_bytes": (_i32, [_vp, _vp, _i64, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -65,6 +65,27 @@ __global__ void fill_f32_kernel(float *__restrict__ p, int64_t n, float v)
             p[i] = v;
 }
 
+__global__ void copy_bytes_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, int64_t n16)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
+}
+
+extern "C" int mambo_copy_bytes(const void *src, void *dst, int64_t bytes, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(bytes >= 0 && bytes % 16 == 0, MAMBO_ERR_VALUE, "bytes must be a non-negative multiple of 16");
+    if (bytes == 0)
+        return MAMBO_OK;
+    MAMBO_REQUIRE(src && dst && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0, MAMBO_ERR_VALUE,
+                  "src and dst must be non-NULL and 16-byte aligned");
+    const int64_t n16 = bytes / 16;
+    const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 4096);
+    hipLaunchKernelGGL(copy_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4 *)src, (uint4 *)dst, n16);
+    return mambo_check_launch("copy_bytes");
+}
+
 extern "C" int mambo_fill_f32(float *ptr, int64_t n, float value, mambo_stream_t stream)
 {
     MAMBO_REQUIRE(n >= 0, MAMBO_ERR_VALUE, "n must be >= 0");
