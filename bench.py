@@ -5,8 +5,11 @@ Default workload: the Llama-3-70B-shaped sweep - 80 layers x 7 projections (q 81
 k/v 1024x8192, o 8192x8192, gate/up 28672x8192, down 8192x28672), 560 distinct IQ3_S
 weights (~29.4 GB resident in HBM) generated on the GPU from the counter-based
 generator, streamed once per step at M tokens (default M=1, decode). One step = the
-560 projections, launched from a captured HIP graph; MXFP8 activations are quantized
-once before timing (the reference times the matmul alone, iq3_s_fp8.py:402-465).
+560 projections in 320 launches (projections that read the same input - q/k/v, gate/up -
+share a grouped launch; --no-group launches each alone), replayed from a captured HIP
+graph; MXFP8 activations are quantized once before timing (the reference times the
+matmul alone, iq3_s_fp8.py:402-465). --workload llama8b runs the same sweep over the
+32 layers of Llama-3-8B (3.0 GB of weights).
 
 value = algorithmic bytes per step / step time, with
   bytes per projection = N*K*110/256 (IQ3_S weights) + M*K*33/32 (E4M3 + E8M0 activations)
@@ -16,6 +19,7 @@ the reference CPU path (ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot
 its CPU case, one IQ3_S linear N=K=4096 with M=8, timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant|copy]
+                    [--layers L] [--no-group] [--no-graph]
 """
 
 from __future__ import annotations
@@ -35,8 +39,8 @@ MXFP8_PEAK_TFLOPS = 5000.0
 
 LLAMA70B_LAYER = [("q", 8192, 8192, 0), ("k", 1024, 8192, 0), ("v", 1024, 8192, 0), ("o", 8192, 8192, 1),
                   ("gate", 28672, 8192, 2), ("up", 28672, 8192, 2), ("down", 8192, 28672, 3)]
-LLAMA8B_SHAPES = [("q/o", 4096, 4096, 0), ("k/v", 1024, 4096, 0), ("gate/up", 14336, 4096, 0),
-                  ("down", 4096, 14336, 1)]
+LLAMA8B_LAYER = [("q", 4096, 4096, 0), ("k", 1024, 4096, 0), ("v", 1024, 4096, 0), ("o", 4096, 4096, 1),
+                 ("gate", 14336, 4096, 2), ("up", 14336, 4096, 2), ("down", 4096, 14336, 3)]
 
 
 def log(msg: str) -> None:
@@ -68,10 +72,13 @@ def synth_activation(m: int, k: int, seed: int):
 
 
 def build_gemm_workload(args):
-    """Weights, activations, outputs and the launch list of the projection sweep."""
+    """Weights, activations and outputs of the projection sweep, as a list of launches.
+    Each launch is (names, [(n, k, fields, out)], (x_values, x_scales)); projections of
+    one layer that read the same input (q/k/v, gate/up) share a launch unless
+    args.no_group."""
     import torch
-    shapes = LLAMA70B_LAYER if args.workload == "llama70b" else LLAMA8B_SHAPES
-    layers = args.layers if args.workload == "llama70b" else args.copies
+    shapes = LLAMA70B_LAYER if args.workload == "llama70b" else LLAMA8B_LAYER
+    layers = args.layers
     m = args.m
     acts = {}
     for _, n, k, slot in shapes:
@@ -83,38 +90,52 @@ def build_gemm_workload(args):
     for layer in range(layers):
         for j, (name, n, k, slot) in enumerate(shapes):
             fields = synth_weight(n, k, seed=1000 * layer + j)
-            key = (n, k)
+            key = (name, n, k)
             if key not in outs:
                 outs[key] = torch.empty((m, n), dtype=torch.float32, device="cuda")
-            launches.append((name, n, k, fields, acts[slot], outs[key]))
+            proj = (n, k, fields, outs[key])
+            if (not args.no_group and launches and launches[-1][3] == (layer, slot)
+                    and len(launches[-1][1]) < 4):
+                launches[-1][0].append(name)
+                launches[-1][1].append(proj)
+            else:
+                launches.append(([name], [proj], acts[slot], (layer, slot)))
         if layer % 10 == 9:
             log(f"prepared {layer + 1}/{layers} layers ({time.time() - t0:.1f} s)")
     torch.cuda.synchronize()
-    return launches
+    return [(names, projs, act) for names, projs, act, _ in launches]
 
 
 def run_gemm(args):
     import torch
-    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul, select_config
+    from mambo_amd.kernels.iq3_s_fp8 import (launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped,
+                                             select_config)
 
     launches = build_gemm_workload(args)
-    configs = [select_config(args.m, n, k) for (_, n, k, _, _, _) in launches]
-    weight_bytes = sum(f.packed.numel() for (_, _, _, f, _, _) in launches)
-    step_bytes = sum(proj_bytes(args.m, n, k) for (_, n, k, _, _, _) in launches)
-    step_flops = sum(2 * args.m * n * k for (_, n, k, _, _, _) in launches)
-    log(f"{len(launches)} projections, {weight_bytes / 1e9:.2f} GB of IQ3_S weights resident")
+    projections = [p for (_, projs, _) in launches for p in projs]
+    configs = [select_config(args.m, sum(n for n, _, _, _ in projs), projs[0][1]) for (_, projs, _) in launches]
+    weight_bytes = sum(f.packed.numel() for (_, _, f, _) in projections)
+    step_bytes = sum(proj_bytes(args.m, n, k) for (n, k, _, _) in projections)
+    step_flops = sum(2 * args.m * n * k for (n, k, _, _) in projections)
+    log(f"{len(projections)} projections in {len(launches)} launches, {weight_bytes / 1e9:.2f} GB of IQ3_S "
+        "weights resident")
 
     def step():
-        for (_, _, _, fields, (xv, xs), out), cfg in zip(launches, configs):
-            launch_iq3_s_fp8_matmul(xv, xs, fields, config=cfg, out=out)
+        for (_, projs, (xv, xs)), cfg in zip(launches, configs):
+            if len(projs) == 1:
+                launch_iq3_s_fp8_matmul(xv, xs, projs[0][2], config=cfg, out=projs[0][3])
+            else:
+                launch_iq3_s_fp8_matmul_grouped(xv, xs, [p[2] for p in projs], config=cfg,
+                                                outs=[p[3] for p in projs])
 
+    outputs = list({id(o): o for (_, _, _, o) in projections}.values())
     stream = torch.cuda.current_stream()
     step()
     torch.cuda.synchronize()
     replay = step
     if not args.no_graph:
         # Capture one step on a side stream, then check one replay against eager results.
-        ref = {id(o): o.clone() for (_, _, _, _, _, o) in launches}
+        ref = [o.clone() for o in outputs]
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(stream)
@@ -122,15 +143,14 @@ def run_gemm(args):
             with torch.cuda.graph(graph, stream=side):
                 step()
         stream.wait_stream(side)
-        for (_, _, _, _, _, o) in launches:
+        for o in outputs:
             o.fill_(float("nan"))
         graph.replay()
         torch.cuda.synchronize()
-        for (name, n, k, _, _, o) in launches:
-            r = ref[id(o)]
+        for o, r in zip(outputs, ref):
             if not torch.allclose(o, r, rtol=1e-5, atol=1e-5):
                 diff = (o - r).abs().max().item()
-                raise RuntimeError(f"graph replay differs from eager launch ({name} {n}x{k}: max diff "
+                raise RuntimeError(f"graph replay differs from eager launch (output {tuple(o.shape)}: max diff "
                                    f"{diff}, nan {int(torch.isnan(o).sum())}, ref nan {int(torch.isnan(r).sum())})")
         replay = graph.replay
         log("captured the step in a HIP graph; replay matches eager")
@@ -153,7 +173,7 @@ def run_gemm(args):
     log(f"{ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), {gbs:.1f} GB/s, {tflops:.2f} TFLOP/s")
     return {
         "ms": ms, "value": gbs, "tflops": tflops, "step_bytes": step_bytes, "step_flops": step_flops,
-        "weight_bytes": weight_bytes, "launches": len(launches),
+        "weight_bytes": weight_bytes, "projections": len(projections), "launches": len(launches),
         "per_launch_bytes": step_bytes / len(launches), "per_launch_us": ms * 1e3 / len(launches),
     }
 
@@ -263,12 +283,15 @@ def main(argv=None) -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--m", type=int, default=1, help="tokens per projection")
     p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy"], default="llama70b")
-    p.add_argument("--layers", type=int, default=80, help="llama70b: layers in the sweep")
-    p.add_argument("--copies", type=int, default=48, help="llama8b: distinct weight copies per shape")
+    p.add_argument("--layers", type=int, default=None, help="layers in the sweep (default 80 for llama70b, 32 for llama8b)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--no-group", action="store_true",
+                   help="one launch per projection (default: q/k/v and gate/up share a launch)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args(argv)
+    if args.layers is None:
+        args.layers = 32 if args.workload == "llama8b" else 80
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -293,13 +316,14 @@ def main(argv=None) -> int:
     else:
         r = run_gemm(args)
         metric = "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline"
+        grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
         if args.workload == "llama70b":
-            workload = f"llama3-70b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}"
+            workload = f"llama3-70b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
         else:
-            workload = f"llama3-8b projection shapes x {args.copies} rotated copies, M={args.m}"
-        config = {"workload": workload, "m": args.m, "projections_per_step": r["launches"],
-                  "weight_gb": round(r["weight_bytes"] / 1e9, 3), "tflops": round(r["tflops"], 3),
-                  "graph": not args.no_graph}
+            workload = f"llama3-8b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
+        config = {"workload": workload, "m": args.m, "projections_per_step": r["projections"],
+                  "launches_per_step": r["launches"], "weight_gb": round(r["weight_bytes"] / 1e9, 3),
+                  "tflops": round(r["tflops"], 3), "graph": not args.no_graph}
     value = r["value"]
     line = {
         "metric": metric,

@@ -42,8 +42,9 @@ enum { MAMBO_DTYPE_F32 = 0, MAMBO_DTYPE_BF16 = 1 };
 /* Kernel families of the projection. */
 enum {
     MAMBO_GEMM_AUTO = 0,    /* library default for the shape */
-    MAMBO_GEMM_STREAM = 1,  /* weight-streaming split-K kernel, M-chunks of 16 */
-    MAMBO_GEMM_TILED = 2    /* LDS-tiled kernel for large M */
+    MAMBO_GEMM_STREAM = 1,  /* weight-streaming kernel, block-diagonal activations (M <= 4 per MFMA) */
+    MAMBO_GEMM_TILED = 2,   /* LDS-tiled kernel for large M */
+    MAMBO_GEMM_DENSE = 3    /* weight-streaming kernel, dense 16-token activations, exact two-term weights */
 };
 
 /* Tunable launch configuration of mambo_iq3s_fp8_matmul (the autotuner's search
@@ -75,6 +76,13 @@ int mambo_device_arch(int device, char *buf, int buf_len);
  * E4M3-encoded form (iq3_s_fp8.py:77-94, `iq3_s_fp8_table`). out: uint32[512]. */
 int mambo_iq3s_grid(uint32_t *out);
 int mambo_iq3s_fp8_grid(uint32_t *out);
+
+/* The exact two-term split of IQ3_S weight magnitudes used by the dense kernels (no
+ * reference counterpart; exported so it can be checked without a GPU). out: uint32[64];
+ * out[4*s + 0..1] hold the E4M3 bytes of hi/2 for grid levels 0..7 (byte j of word w is
+ * level 4w + j) and out[4*s + 2..3] those of lo/2, where (1 + 2s)(2l + 1) = hi + lo and
+ * hi is rounded to 4 significant bits (ties to even). */
+int mambo_iq3s_split_table(uint32_t *out);
 
 /* MXFP8 activation quantizer. Replaces launch_quantize_fp8 / quantize_activation_fp8
  * (quantize_fp8.py:42-52,67-84). x: [m, ldx] of f32 or bf16 (x_dtype); per 32
@@ -125,6 +133,25 @@ int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, in
                           int64_t m, const uint8_t *packed, int64_t n, int64_t blocks,
                           float *out, int64_t ldo, const mambo_gemm_config *cfg,
                           mambo_stream_t stream);
+
+/* Up to MAMBO_MAX_GROUP projections of the same activations in one launch. No
+ * reference counterpart: the reference calls launch_iq3_s_fp8_matmul once per weight
+ * (iq3_s_fp8.py:364-399). This is for callers whose projections share an input, such
+ * as q/k/v of an attention block or gate/up of an MLP: the result equals one
+ * mambo_iq3s_fp8_matmul per projection, with one launch ramp instead of `count`. */
+#define MAMBO_MAX_GROUP 4
+typedef struct mambo_projection {
+    const uint8_t *packed; /* packed weight, n rows x blocks */
+    int64_t n;             /* output features of this projection */
+    float *out;            /* f32 [m, ldo] */
+    int64_t ldo;           /* >= n */
+} mambo_projection;
+
+/* proj[0..count) share xv/xs and K = blocks*256; cfg as for mambo_iq3s_fp8_matmul, with
+ * the default computed for the summed N (mambo_gemm_default_config(m, sum of n, ...)). */
+int mambo_iq3s_fp8_matmul_grouped(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
+                                  int64_t m, const mambo_projection *proj, int count, int64_t blocks,
+                                  const mambo_gemm_config *cfg, mambo_stream_t stream);
 
 /* The configuration mambo_iq3s_fp8_matmul uses when cfg == NULL. */
 int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out);

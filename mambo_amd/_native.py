@@ -27,6 +27,7 @@ DTYPE_BF16 = 1
 GEMM_AUTO = 0
 GEMM_STREAM = 1
 GEMM_TILED = 2
+GEMM_DENSE = 3
 
 
 class GemmConfig(ctypes.Structure):
@@ -56,6 +57,15 @@ class GemmConfig(ctypes.Structure):
         return c
 
 
+MAX_GROUP = 4
+
+
+class Projection(ctypes.Structure):
+    """mirror of mambo_projection"""
+
+    _fields_ = [("packed", ctypes.c_void_p), ("n", ctypes.c_int64), ("out", ctypes.c_void_p), ("ldo", ctypes.c_int64)]
+
+
 # name -> (restype, argtypes); every symbol here is declared in include/mambo_hip.h.
 _vp, _i64, _i32, _u64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint64
 SIGNATURES = {
@@ -65,6 +75,7 @@ SIGNATURES = {
     "mambo_device_arch": (_i32, [_i32, ctypes.c_char_p, _i32]),
     "mambo_iq3s_grid": (_i32, [_vp]),
     "mambo_iq3s_fp8_grid": (_i32, [_vp]),
+    "mambo_iq3s_split_table": (_i32, [_vp]),
     "mambo_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mambo_iq3s_packed_bytes": (_i64, [_i64, _i64]),
     "mambo_iq3s_prepare": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -72,6 +83,8 @@ SIGNATURES = {
     "mambo_iq3s_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "mambo_iq3s_fp8_matmul": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                                      ctypes.POINTER(GemmConfig), _vp]),
+    "mambo_iq3s_fp8_matmul_grouped": (_i32, [_vp, _i64, _vp, _i64, _i64, ctypes.POINTER(Projection), _i32, _i64,
+                                             ctypes.POINTER(GemmConfig), _vp]),
     "mambo_gemm_default_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_gemm_check_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_synth_iq3s": (_i32, [_u64, _i64, _i64, _i64, _vp, _vp]),

@@ -56,6 +56,15 @@ extern "C" int mambo_iq3s_fp8_grid(uint32_t *out)
     return MAMBO_OK;
 }
 
+extern "C" int mambo_iq3s_split_table(uint32_t *out)
+{
+    MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
+    for (int s = 0; s < 16; ++s)
+        for (int w = 0; w < 4; ++w)
+            out[4 * s + w] = kSplitTables.w[s][w];
+    return MAMBO_OK;
+}
+
 __global__ void fill_f32_kernel(float *__restrict__ p, int64_t n, float v)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x * 4 + threadIdx.x;

@@ -36,8 +36,9 @@ __constant__ GridTables c_grid = kGridTables;
 // unit E8M0 scales (2^0).
 // Kept in the global address space (not constant) so the activation pointers stay
 // global and the loads are global_load, not flat_load.
-__device__ __align__(16) uint8_t g_zero_chunk[64] = {};
+__device__ __align__(16) uint8_t g_zero_chunk[128] = {};
 __device__ uint8_t g_unit_scales[2] = {127, 127};
+__constant__ SplitTables c_split = kSplitTables;
 
 // Super-blocks in flight per wave (register ring depth).
 #ifndef MAMBO_STREAM_DEPTH
@@ -180,11 +181,23 @@ __host__ __device__ inline StreamLds stream_lds(int U, int W, int rows, int K, b
     return l;
 }
 
+// Projections of one launch: they share the activations and K; the grid's x dimension
+// runs over the 16-row tiles of all of them, projection g owning tiles
+// [tile_begin[g], tile_begin[g+1]).
+constexpr int kMaxGroup = MAMBO_MAX_GROUP;
+struct GroupArgs {
+    const uint8_t *packed[kMaxGroup];
+    float *out[kMaxGroup];
+    int64_t n[kMaxGroup];
+    int64_t ldo[kMaxGroup];
+    int64_t tile_begin[kMaxGroup];
+    int count;
+};
+
 template <int U, int W, bool kLdsAct>
 __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
-                                                             const uint8_t *__restrict__ packed, int64_t N, int B,
-                                                             int bps, float *__restrict__ out, int64_t ldo, int atomic)
+                                                             GroupArgs ga, int B, int bps, int atomic)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -193,7 +206,19 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     const int64_t m0 = (int64_t)blockIdx.z * 16;
     const int rows = (int)min<int64_t>(U * 4, M - m0);
     const StreamLds L = stream_lds(U, W, rows, K, kLdsAct);
-    const int64_t t = blockIdx.x;
+    // This workgroup's projection (constant indices only, so the arguments stay scalar).
+    const uint8_t *packed = ga.packed[0];
+    float *out = ga.out[0];
+    int64_t N = ga.n[0], ldo = ga.ldo[0], t = blockIdx.x;
+#pragma unroll
+    for (int g = 1; g < kMaxGroup; ++g)
+        if (g < ga.count && (int64_t)blockIdx.x >= ga.tile_begin[g]) {
+            packed = ga.packed[g];
+            out = ga.out[g];
+            N = ga.n[g];
+            ldo = ga.ldo[g];
+            t = blockIdx.x - ga.tile_begin[g];
+        }
     const int b_begin = blockIdx.y * bps;
     const int b_end = min(B, b_begin + bps);
     const int col = lane & 15, q = lane >> 4;
@@ -355,6 +380,270 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     }
 }
 
+// ============================================================================ dense kernel
+// For M > 4 the block-diagonal operand above wastes 3/4 of every MFMA and needs one A
+// sub-tile per 4 tokens. The dense kernel feeds 16 real tokens as the A operand, so one
+// K=128 MFMA spans four weight groups with different scales (1+2s); the weight operand
+// then carries the exact per-weight product P = (1+2s)*g as two E4M3 terms
+// (hi/2 + lo/2, B scale 2; see SplitTables) and the block's fp16 d is applied in f32.
+// Per 256-weight block: 4 MFMAs (2 K halves x hi/lo) for 16 tokens.
+//
+// Decode per code: the grid word in level form (bytes 0..7) from LDS selects, with one
+// v_perm_b32 each, the hi and lo bytes of four weights from the group's 16-byte split
+// table entry; the four signs are OR-ed into hi and XOR-ed into lo (lo has a sign).
+// The decoded group of lane (col, q) is its own group 2q+h; v_permlane16_swap then
+// exchanges half groups between lane groups 0<->1 and 2<->3, so that in MFMA h the K
+// blocks hold weight groups (kb0, kb1, kb2, kb3) = (h, 4+h, 2+h, 6+h) with both 16-byte
+// halves of a group inside one K block (one E8M0 activation scale per K block). The A
+// operand of lane (token i, q) takes the matching bytes: group 4*(q>>1) + h, half q&1,
+// and +64 bytes for group 4*(q>>1) + 2 + h. Scale lane i + 16*kb holds token i's scale
+// of group h + 4*(kb&1) + 2*(kb>>1).
+
+struct ADense {
+    v8i a[2];
+    uint8_t s[2];
+};
+
+struct ALaneD {
+    const uint8_t *x; // this lane's first 16 activation bytes of block 0, MFMA 0
+    const uint8_t *s; // this lane's E8M0 scale of block 0, MFMA 0
+    int xstep;        // 256 or 0
+    int sstep;        // 8 or 0
+};
+
+__device__ __forceinline__ void load_a_dense(ADense &at, const ALaneD &al, int b)
+{
+    const uint8_t *xp = al.x + b * al.xstep;
+    const uint8_t *sp = al.s + b * al.sstep;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 lo = *reinterpret_cast<const uint4 *>(xp + 32 * h);
+        const uint4 hi = *reinterpret_cast<const uint4 *>(xp + 32 * h + 64);
+        at.a[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        at.s[h] = sp[h];
+    }
+}
+
+// hi and lo words of code C of a group: level bytes select from the split table entry
+// (tab.x/.y: hi of levels 0-3/4-7, tab.z/.w: lo), signs moved onto bits 7,15,23,31.
+template <int C>
+__device__ __forceinline__ void split_word(uint32_t lv, uint32_t p, uint4 tab, int &hi, int &lo)
+{
+    const uint32_t m = funnel_shr(p, p, (25 + C) & 31) & 0x80808080u;
+    hi = (int)(__builtin_amdgcn_perm(tab.y, tab.x, lv) | m);
+    lo = (int)(__builtin_amdgcn_perm(tab.w, tab.z, lv) ^ m);
+}
+
+template <int H, int... C>
+__device__ __forceinline__ void decode_split(const uint32_t (&s)[5], uint32_t p, const uint8_t *lvl, uint4 tab,
+                                             v8i &bhi, v8i &blo, std::integer_sequence<int, C...>)
+{
+    int h[8], l[8];
+    (split_word<C>(*reinterpret_cast<const uint32_t *>(lvl + code_addr<8 * H + C>(s)), p, tab, h[C], l[C]), ...);
+    bhi = v8i{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+    blo = v8i{l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
+}
+
+// Own-group order (bytes 0-15 / 16-31 = first / second half of the lane's group) to the
+// dense MFMA K order: lane group 1's first half <-> lane group 0's second half (and 3/2).
+__device__ __forceinline__ void to_dense_order(v8i &b)
+{
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)b[k], (uint32_t)b[4 + k], false, false);
+        b[k] = (int)r[0];
+        b[4 + k] = (int)r[1];
+    }
+}
+
+__device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, const uint8_t *lvl,
+                                              const uint8_t *split, float (&acc)[4], bool valid)
+{
+    const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
+    const uint32_t sc = w.sc;
+    const uint4 t0 = *reinterpret_cast<const uint4 *>(split + 16 * (sc & 15u));
+    const uint4 t1 = *reinterpret_cast<const uint4 *>(split + 16 * (sc >> 4));
+    v8i h0, l0, h1, l1;
+    decode_split<0>(s, w.sg.x, lvl, t0, h0, l0, std::make_integer_sequence<int, 8>{});
+    decode_split<1>(s, w.sg.y, lvl, t1, h1, l1, std::make_integer_sequence<int, 8>{});
+    to_dense_order(h0);
+    to_dense_order(l0);
+    to_dense_order(h1);
+    to_dense_order(l1);
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    // B scale 2^1: the split terms are stored halved
+    v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
+    v4f c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
+    c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c1, 0, 0, 0, (int)at.s[1], 0, 128);
+    c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c2, 0, 0, 0, (int)at.s[1], 0, 128);
+    const float f = valid ? half_bits_to_float((uint16_t)w.dh) : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        acc[r] = __builtin_fmaf(c1[r] + c2[r], f, acc[r]);
+}
+
+// LDS of the dense kernel: level grid (2 KiB), split tables (256 B), cross-wave partial
+// sums [W][4][64] f32, 128 zero bytes + unit scales for rows past M (a lane reads up to
+// byte 32 + 64 + 16 of its chunk), and - when kLdsAct -
+// the chunk's activation rows [rows][K] and scales [rows][K/32].
+struct DenseLds {
+    int split, red, zero, x, xs, total;
+};
+
+__host__ __device__ inline DenseLds dense_lds(int W, int rows, int K, bool lds_act)
+{
+    DenseLds l;
+    l.split = 2048;
+    l.red = l.split + 256;
+    l.zero = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
+    l.x = l.zero + 144;
+    l.xs = l.x + (lds_act ? rows * K : 0);
+    l.total = l.xs + (lds_act ? rows * (K / 32) : 0);
+    return l;
+}
+
+template <int W, bool kLdsAct>
+__global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+                                                            const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
+                                                            GroupArgs ga, int B, int bps, int atomic)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = B * 256;
+    const int64_t m0 = (int64_t)blockIdx.z * 16;
+    const int rows = (int)min<int64_t>(16, M - m0);
+    const DenseLds L = dense_lds(W, rows, K, kLdsAct);
+    const uint8_t *packed = ga.packed[0];
+    float *out = ga.out[0];
+    int64_t N = ga.n[0], ldo = ga.ldo[0], t = blockIdx.x;
+#pragma unroll
+    for (int g = 1; g < kMaxGroup; ++g)
+        if (g < ga.count && (int64_t)blockIdx.x >= ga.tile_begin[g]) {
+            packed = ga.packed[g];
+            out = ga.out[g];
+            N = ga.n[g];
+            ldo = ga.ldo[g];
+            t = blockIdx.x - ga.tile_begin[g];
+        }
+    const int b_begin = blockIdx.y * bps;
+    const int b_end = min(B, b_begin + bps);
+    const int col = lane & 15, q = lane >> 4;
+    const uint8_t *wt = packed + t * (int64_t)B * kTileBytes;
+    const int first = b_begin + wave;
+    const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
+    const int last = first + (count - 1) * W;
+    {
+        const int nt = W * 64;
+        uint32_t *lw = reinterpret_cast<uint32_t *>(smem);
+        for (int i = tid; i < 512; i += nt)
+            lw[i] = c_grid.level[i];
+        if (tid < 64)
+            reinterpret_cast<uint32_t *>(smem + L.split)[tid] = c_split.w[tid >> 2][tid & 3];
+        if (tid < 36)
+            reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 32 ? 0u : 0x7F7F7F7Fu;
+        if constexpr (kLdsAct) {
+            const int nx = rows * K / 16;
+            for (int c = tid; c < nx; c += nt) {
+                const int r = c * 16 / K;
+                *reinterpret_cast<uint4 *>(smem + L.x + c * 16) =
+                    *reinterpret_cast<const uint4 *>(xv + (m0 + r) * ldxv + (c * 16 - r * K));
+            }
+            const int ns = rows * (K / 32);
+            for (int i = tid; i < ns; i += nt) {
+                const int r = i / (K / 32);
+                smem[L.xs + i] = xs[(m0 + r) * ldxs + (i - r * (K / 32))];
+            }
+        }
+    }
+    __syncthreads();
+    const uint8_t *lvl = smem;
+    const uint8_t *split = smem + L.split;
+
+    // A lane: token col of the chunk; bytes of group 4*(q>>1) + h, half q&1 (+64 for the
+    // second 16 bytes); scale of group 4*(q&1) + 2*(q>>1) + h.
+    ALaneD al;
+    {
+        const bool on = col < rows;
+        const int xoff = 32 * (4 * (q >> 1)) + 16 * (q & 1);
+        const int soff = 4 * (q & 1) + 2 * (q >> 1);
+        if constexpr (kLdsAct) {
+            al.x = on ? smem + L.x + col * K + xoff : smem + L.zero;
+            al.s = on ? smem + L.xs + col * (K / 32) + soff : smem + L.zero + 128;
+        } else {
+            al.x = on ? xv + (m0 + col) * ldxv + xoff : g_zero_chunk;
+            al.s = on ? xs + (m0 + col) * ldxs + soff : g_unit_scales;
+        }
+        al.xstep = on ? 256 : 0;
+        al.sstep = on ? 8 : 0;
+    }
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (count > 0) {
+        WTile wr[kDepth];
+        ADense ar[kLdsAct ? 1 : kDepth];
+#pragma unroll
+        for (int j = 0; j < kDepth - 1; ++j) {
+            wr[j] = load_w(wt + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
+            if constexpr (!kLdsAct)
+                load_a_dense(ar[j], al, min(first + j * W, last));
+        }
+        for (int i0 = 0; i0 < count; i0 += kDepth) {
+#pragma unroll
+            for (int j = 0; j < kDepth; ++j) {
+                const int i = i0 + j;
+                const int slot = (j + kDepth - 1) % kDepth;
+                const int bp = min(first + (i + kDepth - 1) * W, last);
+                wr[slot] = load_w(wt + (int64_t)bp * kTileBytes, lane, col);
+                if constexpr (!kLdsAct)
+                    load_a_dense(ar[slot], al, bp);
+                if constexpr (MAMBO_SCHED_FENCE)
+                    __builtin_amdgcn_sched_barrier(0);
+                if constexpr (kLdsAct) {
+                    load_a_dense(ar[0], al, min(first + i * W, last));
+                    compute_dense(wr[j], ar[0], lvl, split, acc, i < count);
+                } else {
+                    compute_dense(wr[j], ar[j], lvl, split, acc, i < count);
+                }
+                if constexpr (MAMBO_SCHED_FENCE)
+                    __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+
+    // D[i][j] of the MFMA sits in lane j + 16*(i/4), register i%4: token 4q + r, weight
+    // row col. The waves hold partial sums over disjoint K blocks.
+    if constexpr (W > 1) {
+        float *red = reinterpret_cast<float *>(smem + L.red);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            red[(wave * 4 + r) * 64 + lane] = acc[r];
+        __syncthreads();
+        if (wave != 0)
+            return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; ++w)
+                v += red[(w * 4 + r) * 64 + lane];
+            acc[r] = v;
+        }
+    }
+    const int64_t n = t * kTileRows + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + 4 * q + r;
+        if (m < M && n < N) {
+            float *o = out + m * ldo + n;
+            if (atomic)
+                atomicAdd(o, acc[r]);
+            else
+                *o = acc[r];
+        }
+    }
+}
+
 __global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t cols, int64_t ld)
 {
     const int64_t r = blockIdx.y;
@@ -365,22 +654,20 @@ __global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t 
 
 template <int U, int W, bool kLdsAct>
 void launch_stream_uwa(dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
-                       int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B, int bps, float *out,
-                       int64_t ldo, int atomic)
+                       int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
-                       packed, N, B, bps, out, ldo, atomic);
+                       ga, B, bps, atomic);
 }
 
 template <int U, int W>
 void launch_stream_uw(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                      const uint8_t *xs, int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B, int bps,
-                      float *out, int64_t ldo, int atomic)
+                      const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     if (lds_act)
-        launch_stream_uwa<U, W, true>(grid, lds, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic);
+        launch_stream_uwa<U, W, true>(grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
     else
-        launch_stream_uwa<U, W, false>(grid, lds, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo, atomic);
+        launch_stream_uwa<U, W, false>(grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
 }
 
 // Waves per workgroup the stream kernel is built for.
@@ -388,13 +675,40 @@ constexpr int kStreamWaves[] = {1, 2, 4, 6, 8, 12, 16};
 
 template <int U>
 int launch_stream_u(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
-                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const uint8_t *packed, int64_t N, int B,
-                    int bps, float *out, int64_t ldo, int atomic)
+                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
+                    int atomic)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_stream_uw<U, WV>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, packed, N, B, bps, out, ldo,    \
-                                atomic);                                                                           \
+        launch_stream_uw<U, WV>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);             \
+        break;
+    switch (waves) {
+        MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
+    default:
+        return mambo_fail(MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16 (got %d)", waves);
+    }
+#undef MAMBO_W
+    return MAMBO_OK;
+}
+
+template <int W>
+void launch_dense_w(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                    const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+{
+    if (lds_act)
+        hipLaunchKernelGGL((gemm_dense_kernel<W, true>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M, ga, B,
+                           bps, atomic);
+    else
+        hipLaunchKernelGGL((gemm_dense_kernel<W, false>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M, ga,
+                           B, bps, atomic);
+}
+
+int launch_dense(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                 const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+{
+#define MAMBO_W(WV)                                                                                                \
+    case WV:                                                                                                       \
+        launch_dense_w<WV>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                  \
         break;
     switch (waves) {
         MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
@@ -430,17 +744,21 @@ extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, m
     MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
     MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
     mambo_gemm_config c = {};
-    c.kernel = MAMBO_GEMM_STREAM;
+    // Block-diagonal activations cost nothing extra while one MFMA covers every token
+    // (M <= 4); beyond that the dense kernel does 4 MFMAs per block for 16 tokens where
+    // the block-diagonal one needs 2 per 4 tokens and an activation sub-tile each.
+    c.kernel = m <= 4 ? MAMBO_GEMM_STREAM : MAMBO_GEMM_DENSE;
     const int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
-    // Waves per workgroup: the largest power of two up to 8 (16 for grids of at most 2K
-    // waves) that divides the K blocks evenly, keeps at least two blocks per wave and at
+    // Waves per workgroup: the largest power of two up to 8 (16 for M <= 4 and grids of at
+    // most 2K waves; wider sub-tiles spill at 1024 threads) that divides the K blocks evenly, keeps at least two blocks per wave and at
     // most about two residency rounds of waves in the grid (measured on gfx950: deeper
     // oversubscription and uneven splits both lose). K is split only when even that
     // leaves the chip mostly idle: a split costs a zero fill and atomics, which lose to
     // wider workgroups down to ~1K waves.
     int waves = 1;
     for (int w : {2, 4, 8, 16})
-        if (units * w <= (w < 16 ? kTargetWaves : kTargetWaves / 4) && blocks % w == 0 && blocks / w >= 2)
+        if (units * w <= (w < 16 ? kTargetWaves : kTargetWaves / 4) && (w < 16 || m <= 4) && blocks % w == 0 &&
+            blocks / w >= 2)
             waves = w;
     int64_t split = 1;
     if (units * waves < kMinWaves) {
@@ -457,29 +775,50 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
 {
     MAMBO_REQUIRE(cfg != nullptr, MAMBO_ERR_VALUE, "cfg must not be NULL");
     MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
-    MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM, MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
+    MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM || cfg->kernel == MAMBO_GEMM_DENSE, MAMBO_ERR_VALUE,
+                  "unsupported kernel family %d", cfg->kernel);
     MAMBO_REQUIRE(valid_waves(cfg->waves), MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16");
     MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                   "split_k must be in [1, K/256]");
     return MAMBO_OK;
 }
 
-extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t m,
-                                     const uint8_t *packed, int64_t n, int64_t blocks, float *out, int64_t ldo,
-                                     const mambo_gemm_config *cfg, mambo_stream_t stream)
+namespace {
+
+int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t m,
+                    const mambo_projection *proj, int count, int64_t blocks, const mambo_gemm_config *cfg,
+                    hipStream_t s)
 {
-    MAMBO_REQUIRE(xv && xs && packed && out, MAMBO_ERR_VALUE, "null pointer");
-    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive (M=%lld N=%lld B=%lld)",
-                  (long long)m, (long long)n, (long long)blocks);
+    MAMBO_REQUIRE(xv && xs && proj, MAMBO_ERR_VALUE, "null pointer");
+    MAMBO_REQUIRE(count >= 1 && count <= kMaxGroup, MAMBO_ERR_VALUE, "count must be in [1, %d] (got %d)", kMaxGroup,
+                  count);
+    MAMBO_REQUIRE(m >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive (M=%lld B=%lld)", (long long)m,
+                  (long long)blocks);
     MAMBO_REQUIRE(blocks <= (1 << 20), MAMBO_ERR_VALUE, "K too large");
     const int64_t k = blocks * 256;
-    MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32 && ldo >= n, MAMBO_ERR_VALUE, "row strides must cover the row");
+    MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32, MAMBO_ERR_VALUE, "activation row strides must cover the row");
     MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
                   "x_values base and row stride must be 16-byte aligned");
-    MAMBO_REQUIRE((uintptr_t)packed % 16 == 0, MAMBO_ERR_VALUE, "packed weight must be 16-byte aligned");
+    GroupArgs ga = {};
+    ga.count = count;
+    int64_t tiles = 0, n_total = 0;
+    for (int g = 0; g < count; ++g) {
+        const mambo_projection &p = proj[g];
+        MAMBO_REQUIRE(p.packed && p.out, MAMBO_ERR_VALUE, "projection %d: null pointer", g);
+        MAMBO_REQUIRE(p.n >= 1, MAMBO_ERR_VALUE, "projection %d: n must be positive (N=%lld)", g, (long long)p.n);
+        MAMBO_REQUIRE(p.ldo >= p.n, MAMBO_ERR_VALUE, "projection %d: output row stride must cover the row", g);
+        MAMBO_REQUIRE((uintptr_t)p.packed % 16 == 0, MAMBO_ERR_VALUE, "projection %d: packed weight must be 16-byte aligned", g);
+        ga.packed[g] = p.packed;
+        ga.out[g] = p.out;
+        ga.n[g] = p.n;
+        ga.ldo[g] = p.ldo;
+        ga.tile_begin[g] = tiles;
+        tiles += cdiv(p.n, kTileRows);
+        n_total += p.n;
+    }
     // Library default for the shape, overlaid with the non-zero fields of cfg.
     mambo_gemm_config c;
-    int rc = mambo_gemm_default_config(m, n, blocks, &c);
+    int rc = mambo_gemm_default_config(m, n_total, blocks, &c);
     if (rc)
         return rc;
     if (cfg != nullptr) {
@@ -493,12 +832,10 @@ extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint
             c.tile_m = cfg->tile_m;
         if (cfg->tile_n)
             c.tile_n = cfg->tile_n;
-        rc = mambo_gemm_check_config(m, n, blocks, &c);
+        rc = mambo_gemm_check_config(m, n_total, blocks, &c);
         if (rc)
             return rc;
     }
-    hipStream_t s = (hipStream_t)stream;
-    const int64_t tiles = cdiv(n, kTileRows);
     const int64_t mchunks = cdiv(m, 16);
     MAMBO_REQUIRE(tiles <= 0x7FFFFFFF && mchunks <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
     const int bps = (int)cdiv(blocks, c.split_k);
@@ -506,31 +843,61 @@ extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint
     const int atomic = splits > 1;
     if (atomic) {
         MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
-        dim3 zg((unsigned)std::min<int64_t>(cdiv(n, 256), 1024), (unsigned)m);
-        hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, out, m, n, ldo);
-        rc = mambo_check_launch("zero_rows");
-        if (rc)
-            return rc;
+        for (int g = 0; g < count; ++g) {
+            dim3 zg((unsigned)std::min<int64_t>(cdiv(ga.n[g], 256), 1024), (unsigned)m);
+            hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, ga.out[g], m, ga.n[g], ga.ldo[g]);
+            rc = mambo_check_launch("zero_rows");
+            if (rc)
+                return rc;
+        }
     }
-    const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
     const int rows = (int)std::min<int64_t>(16, m); // rows of the largest M chunk
     // Stage the activations in LDS when they are small enough; otherwise read them from
     // global memory (L2) in the weight ring.
     bool lds_act = (int64_t)rows * k * 33 / 32 <= kMaxLdsAct;
-    if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > 64 * 1024)
-        lds_act = false;
-    const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
-    MAMBO_REQUIRE(L.total <= 64 * 1024, MAMBO_ERR_VALUE,
-                  "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
-                  c.waves, (long long)m);
     dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
-    switch (U) {
-    case 1: rc = launch_stream_u<1>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
-    case 2: rc = launch_stream_u<2>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
-    case 3: rc = launch_stream_u<3>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
-    default: rc = launch_stream_u<4>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, packed, n, (int)blocks, bps, out, ldo, atomic); break;
+    const int B = (int)blocks;
+    if (c.kernel == MAMBO_GEMM_DENSE) {
+        if (lds_act && dense_lds(c.waves, rows, (int)k, true).total > 64 * 1024)
+            lds_act = false;
+        const DenseLds L = dense_lds(c.waves, rows, (int)k, lds_act);
+        rc = launch_dense(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic);
+    } else {
+        const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
+        if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > 64 * 1024)
+            lds_act = false;
+        const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
+        MAMBO_REQUIRE(L.total <= 64 * 1024, MAMBO_ERR_VALUE,
+                      "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
+                      c.waves, (long long)m);
+        switch (U) {
+        case 1: rc = launch_stream_u<1>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
+        case 2: rc = launch_stream_u<2>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
+        case 3: rc = launch_stream_u<3>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
+        default: rc = launch_stream_u<4>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
+        }
     }
     if (rc)
         return rc;
     return mambo_check_launch("iq3s_fp8_matmul");
+}
+
+} // namespace
+
+extern "C" int mambo_iq3s_fp8_matmul(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t m,
+                                     const uint8_t *packed, int64_t n, int64_t blocks, float *out, int64_t ldo,
+                                     const mambo_gemm_config *cfg, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(packed && out, MAMBO_ERR_VALUE, "null pointer");
+    MAMBO_REQUIRE(n >= 1, MAMBO_ERR_VALUE, "shape must be positive (N=%lld)", (long long)n);
+    MAMBO_REQUIRE(ldo >= n, MAMBO_ERR_VALUE, "row strides must cover the row");
+    const mambo_projection p = {packed, n, out, ldo};
+    return run_projections(xv, ldxv, xs, ldxs, m, &p, 1, blocks, cfg, (hipStream_t)stream);
+}
+
+extern "C" int mambo_iq3s_fp8_matmul_grouped(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
+                                             int64_t m, const mambo_projection *proj, int count, int64_t blocks,
+                                             const mambo_gemm_config *cfg, mambo_stream_t stream)
+{
+    return run_projections(xv, ldxv, xs, ldxs, m, proj, count, blocks, cfg, (hipStream_t)stream);
 }

@@ -75,6 +75,65 @@ __host__ __device__ constexpr GridTables make_grid_tables()
 
 inline constexpr GridTables kGridTables = make_grid_tables();
 
+// Exact two-term split of the IQ3_S weight magnitudes for dense FP8 operands. A weight
+// is d * (1 + 2s) * (2l + 1) * sign (s: 4-bit group scale, l: 3-bit grid level); the
+// integer P = (1 + 2s)(2l + 1) <= 465 needs up to 9 significant bits, E4M3 holds 4.
+// P = hi + lo with hi = P rounded to 4 significant bits (ties to even) and lo = P - hi
+// (an integer, |lo| <= 16); hi/2 and lo/2 are exact E4M3 values, so an MFMA with B
+// scale 2 over both terms gives P exactly. For each s the table holds the E4M3 bytes of
+// hi/2 and lo/2 for the eight levels: w[s] = {hi l=0..3, hi l=4..7, lo l=0..3, lo l=4..7},
+// byte j of a word = level 4*(word & 1) + j, ready for v_perm_b32 with the level bytes
+// of a grid word as selectors.
+__host__ __device__ constexpr uint32_t round_to_4_significant_bits(uint32_t p)
+{
+    int bits = 0;
+    while ((p >> bits) != 0u)
+        ++bits;
+    if (bits <= 4)
+        return p;
+    const int shift = bits - 4;
+    uint32_t q = p >> shift;
+    const uint32_t rem = p & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u)))
+        ++q;
+    return q << shift;
+}
+
+// E4M3 bits of k/2 for an integer k whose magnitude has at most 4 significant bits and
+// |k| <= 480 (so k/2 is exact in E4M3).
+__host__ __device__ constexpr uint32_t e4m3_of_half_integer(int k)
+{
+    if (k == 0)
+        return 0u;
+    const uint32_t sign = k < 0 ? 0x80u : 0u;
+    const uint32_t a = (uint32_t)(k < 0 ? -k : k);
+    int t = 0;
+    while ((a >> (t + 1)) != 0u)
+        ++t;
+    // k/2 = 2^(t-1) * (a / 2^t); E4M3 exponent field t - 1 + 7, mantissa (a*8 >> t) - 8
+    return sign | ((uint32_t)(t + 6) << 3) | (((a << 3) >> t) - 8u);
+}
+
+struct SplitTables {
+    uint32_t w[16][4];
+};
+
+__host__ __device__ constexpr SplitTables make_split_tables()
+{
+    SplitTables t{};
+    for (int s = 0; s < 16; ++s)
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t p = (1u + 2u * s) * (2u * l + 1u);
+            const uint32_t hi = round_to_4_significant_bits(p);
+            const int lo = (int)p - (int)hi;
+            t.w[s][l >> 2] |= e4m3_of_half_integer((int)hi) << (8 * (l & 3));
+            t.w[s][2 + (l >> 2)] |= e4m3_of_half_integer(lo) << (8 * (l & 3));
+        }
+    return t;
+}
+
+inline constexpr SplitTables kSplitTables = make_split_tables();
+
 // ----------------------------------------------------------------------------- device helpers
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));

@@ -43,13 +43,13 @@ _IQ3_TABLES: dict[int, torch.Tensor] = {}
 
 # Launch configurations per architecture, selected by token count as in the reference
 # (iq3_s_fp8.py:49-60). Fields follow mambo_gemm_config; 0 = the library's per-shape
-# default (waves sized so the whole grid is resident in one round, K split only for
-# small N). Per-shape autotuned entries (tuned_gfx950.json, written by
+# default (kernel family by M, waves sized to about two residency rounds, K split only
+# for small grids). Per-shape autotuned entries (tuned_gfx950.json, written by
 # mambo_amd.utils.kernel_benchmark) take precedence.
 BEST_CONFIGS = {
     "gfx950": {
-        "medium": {"kernel": _native.GEMM_STREAM, "waves": 0, "split_k": 0},
-        "large": {"kernel": _native.GEMM_STREAM, "waves": 0, "split_k": 0},
+        "medium": {"kernel": _native.GEMM_AUTO, "waves": 0, "split_k": 0},
+        "large": {"kernel": _native.GEMM_AUTO, "waves": 0, "split_k": 0},
     },
 }
 LARGE_TOKEN_THRESHOLD = 32
@@ -148,6 +148,33 @@ def select_config(m: int, n: int, k: int, arch: str | None = None) -> dict:
     return dict(BEST_CONFIGS[arch]["medium" if m < LARGE_TOKEN_THRESHOLD else "large"])
 
 
+def _prepare_activations(x_values, x_scales, k: int):
+    """Validate MXFP8 activations [M,K] + [M,K/32]; return them in a form the kernels
+    read in place (unit column stride, 16-byte aligned rows), copying only if needed."""
+    if not isinstance(x_values, torch.Tensor) or x_values.ndim != 2 or x_values.dtype != torch.uint8 \
+            or x_values.shape[0] < 1 or x_values.shape[1] != k:
+        raise ValueError("x_values must be uint8 [M,K]")
+    m = int(x_values.shape[0])
+    if not isinstance(x_scales, torch.Tensor) or tuple(x_scales.shape) != (m, k // 32) \
+            or x_scales.dtype != torch.uint8:
+        raise ValueError("x_scales must be uint8 [M,K/32]")
+    if x_scales.device != x_values.device:
+        raise ValueError("x_values and x_scales must be on the same device")
+    if x_values.stride(1) != 1 or x_values.stride(0) % 16 or x_values.data_ptr() % 16:
+        x_values = x_values.contiguous() if x_values.stride(1) != 1 else x_values.clone()
+    if x_scales.stride(1) != 1:
+        x_scales = x_scales.contiguous()
+    return x_values, x_scales, m
+
+
+def _output(out, m: int, n: int, dev) -> torch.Tensor:
+    if out is None:
+        return torch.empty((m, n), dtype=torch.float32, device=dev)
+    if tuple(out.shape) != (m, n) or out.dtype != torch.float32 or out.stride(1) != 1 or out.device != dev:
+        raise ValueError("out must be float32 [M,N] with unit column stride on the activations' device")
+    return out
+
+
 def launch_iq3_s_fp8_matmul(x_values: torch.Tensor, x_scales: torch.Tensor, iq3_weight: IQ3SFields,
                             *, stream=None, config: dict | None = None,
                             out: torch.Tensor | None = None) -> torch.Tensor:
@@ -161,25 +188,12 @@ def launch_iq3_s_fp8_matmul(x_values: torch.Tensor, x_scales: torch.Tensor, iq3_
     """
     n_rows, k_blocks = _weight_dimensions(iq3_weight)
     k = k_blocks * IQ3_S_BLOCK_VALUES
-    if not isinstance(x_values, torch.Tensor) or x_values.ndim != 2 or x_values.dtype != torch.uint8 \
-            or x_values.shape[0] < 1 or x_values.shape[1] != k:
-        raise ValueError("x_values must be uint8 [M,K]")
-    m = int(x_values.shape[0])
-    if not isinstance(x_scales, torch.Tensor) or tuple(x_scales.shape) != (m, k // 32) \
-            or x_scales.dtype != torch.uint8:
-        raise ValueError("x_scales must be uint8 [M,K/32]")
+    x_values, x_scales, m = _prepare_activations(x_values, x_scales, k)
     dev = x_values.device
     with torch.cuda.device(dev):
         cfg = _native.GemmConfig.from_dict(config if config is not None else select_config(m, n_rows, k))
         packed = ensure_packed(iq3_weight, stream)
-        if x_values.stride(1) != 1 or x_values.stride(0) % 16 or x_values.data_ptr() % 16:
-            x_values = x_values.contiguous() if x_values.stride(1) != 1 else x_values.clone()
-        if x_scales.stride(1) != 1:
-            x_scales = x_scales.contiguous()
-        if out is None:
-            out = torch.empty((m, n_rows), dtype=torch.float32, device=dev)
-        elif tuple(out.shape) != (m, n_rows) or out.dtype != torch.float32 or out.stride(1) != 1:
-            raise ValueError("out must be float32 [M,N] with unit column stride")
+        out = _output(out, m, n_rows, dev)
         _native.check(_native.lib().mambo_iq3s_fp8_matmul(
             x_values.data_ptr(), x_values.stride(0), x_scales.data_ptr(), x_scales.stride(0), m,
             packed.data_ptr(), n_rows, k_blocks, out.data_ptr(), out.stride(0), cfg,
@@ -187,18 +201,58 @@ def launch_iq3_s_fp8_matmul(x_values: torch.Tensor, x_scales: torch.Tensor, iq3_
     return out
 
 
+def launch_iq3_s_fp8_matmul_grouped(x_values: torch.Tensor, x_scales: torch.Tensor, iq3_weights,
+                                    *, stream=None, config: dict | None = None, outs=None) -> list[torch.Tensor]:
+    """Several projections of the same MXFP8 activations in one launch (no reference
+    counterpart; the reference calls launch_iq3_s_fp8_matmul per weight,
+    iq3_s_fp8.py:364-399). For projections that share an input - q/k/v, gate/up - this
+    returns what one launch_iq3_s_fp8_matmul per weight returns, with one launch.
+
+    ``iq3_weights``: 1..4 IQ3SFields with the same K. ``outs``: optional float32
+    [M, N_i] outputs. ``config``: as for launch_iq3_s_fp8_matmul, defaulting to the
+    tuned or library configuration for the summed N.
+    """
+    weights = list(iq3_weights)
+    if not 1 <= len(weights) <= _native.MAX_GROUP:
+        raise ValueError(f"between 1 and {_native.MAX_GROUP} weights per grouped launch")
+    dims = [_weight_dimensions(w) for w in weights]
+    k_blocks = dims[0][1]
+    if any(b != k_blocks for _, b in dims):
+        raise ValueError("grouped weights must share K")
+    k = k_blocks * IQ3_S_BLOCK_VALUES
+    x_values, x_scales, m = _prepare_activations(x_values, x_scales, k)
+    dev = x_values.device
+    if outs is not None and len(outs) != len(weights):
+        raise ValueError("outs must hold one output per weight")
+    n_total = sum(n for n, _ in dims)
+    with torch.cuda.device(dev):
+        cfg = _native.GemmConfig.from_dict(config if config is not None else select_config(m, n_total, k))
+        result = [_output(None if outs is None else outs[i], m, n, dev) for i, (n, _) in enumerate(dims)]
+        projections = (_native.Projection * len(weights))()
+        for i, (w, (n, _)) in enumerate(zip(weights, dims)):
+            projections[i] = _native.Projection(ensure_packed(w, stream).data_ptr(), n, result[i].data_ptr(),
+                                                result[i].stride(0))
+        _native.check(_native.lib().mambo_iq3s_fp8_matmul_grouped(
+            x_values.data_ptr(), x_values.stride(0), x_scales.data_ptr(), x_scales.stride(0), m,
+            projections, len(weights), k_blocks, cfg, _native.stream_handle(stream)),
+            "launch_iq3_s_fp8_matmul_grouped")
+    return result
+
+
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
-    search spaces of iq3_s_fp8.py:416-459): waves per workgroup x K split."""
+    search spaces of iq3_s_fp8.py:416-459): kernel family (block-diagonal or dense
+    activations) x waves per workgroup x K split."""
     blocks = k // IQ3_S_BLOCK_VALUES
     u = min(4, -(-m // 4))
     space = []
-    for waves in (1, 2, 4, 6, 8, 12, 16):
-        if waves * u > 32 or waves > blocks:
-            continue
-        for split in (1, 2, 4, 8):
-            if split <= blocks // waves:
-                space.append({"kernel": _native.GEMM_STREAM, "waves": waves, "split_k": split})
+    for kernel in (_native.GEMM_STREAM, _native.GEMM_DENSE):
+        for waves in (1, 2, 4, 6, 8, 12, 16):
+            if waves > blocks or (kernel == _native.GEMM_STREAM and waves * u > 32):
+                continue
+            for split in (1, 2, 4, 8):
+                if split <= blocks // waves:
+                    space.append({"kernel": kernel, "waves": waves, "split_k": split})
     return space
 
 
@@ -224,7 +278,8 @@ def make_benchmark_cases(iq3_weight: torch.Tensor, tokens: tuple[int, ...] = (4,
             launch_iq3_s_fp8_matmul(x_values, x_scales, fields, stream=stream, config=config, out=out)
 
         return BenchmarkCase(name=f"M={m} N={n_rows} K={k}", stream=stream, launch=launch,
-                             search_space=gemm_search_space(m, n_rows, k), summary_keys=("waves", "split_k"),
+                             search_space=gemm_search_space(m, n_rows, k),
+                             summary_keys=("kernel", "waves", "split_k"),
                              key=tuned_key(n_rows, k, m))
 
     return [make_case(m) for m in tokens]

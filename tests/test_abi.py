@@ -70,6 +70,16 @@ def test_gemm_config_defaults_and_validation():
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
     ok = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 8, "split_k": 4})
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(ok)) == 0
+    ok = _native.GemmConfig.from_dict({"kernel": _native.GEMM_DENSE, "waves": 8, "split_k": 4})
+    assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(ok)) == 0
+    bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 8, "split_k": 1})
+    assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
+    # block-diagonal activations up to M=4, dense beyond
+    for m, kernel in ((1, _native.GEMM_STREAM), (4, _native.GEMM_STREAM), (5, _native.GEMM_DENSE),
+                      (16, _native.GEMM_DENSE), (2048, _native.GEMM_DENSE)):
+        c = _native.GemmConfig()
+        assert lib.mambo_gemm_default_config(m, 4096, 16, ctypes.byref(c)) == 0
+        assert c.kernel == kernel, (m, c.as_dict())
 
 
 def test_codebook_exports_match_python_tables():
@@ -84,8 +94,9 @@ def test_codebook_exports_match_python_tables():
 
 def test_python_api_validation_without_gpu():
     import torch
-    from mambo_amd.kernels.iq3_s_fp8 import (launch_dequant_iq3_s, launch_iq3_s_fp8_matmul, m_bucket,
-                                             select_config)
+    from mambo_amd.kernels.iq3_s_fp8 import (launch_dequant_iq3_s, launch_iq3_s_fp8_matmul,
+                                             launch_iq3_s_fp8_matmul_grouped, m_bucket, select_config)
+    from mambo_amd.utils.iq3_s_weight import IQ3SFields
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
     with pytest.raises(ValueError):
@@ -103,7 +114,51 @@ def test_python_api_validation_without_gpu():
                                 "not prepared")
     with pytest.raises(TypeError):
         launch_dequant_iq3_s(object())
+
+    def fields(n, blocks):  # field shapes only; validation runs before any launch
+        return IQ3SFields(torch.zeros(blocks, n, dtype=torch.float16), torch.zeros(blocks, n, 16, dtype=torch.int32),
+                          torch.zeros(blocks, n, 4, dtype=torch.int16), torch.zeros(blocks, n, 8, dtype=torch.int32),
+                          torch.zeros(blocks, n, dtype=torch.int32))
+    xv, xs = torch.zeros(1, 512, dtype=torch.uint8), torch.zeros(1, 16, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="share K"):
+        launch_iq3_s_fp8_matmul_grouped(xv, xs, [fields(16, 2), fields(16, 1)])
+    with pytest.raises(ValueError, match="between 1 and 4"):
+        launch_iq3_s_fp8_matmul_grouped(xv, xs, [fields(16, 2)] * 5)
+    with pytest.raises(ValueError, match="between 1 and 4"):
+        launch_iq3_s_fp8_matmul_grouped(xv, xs, [])
+    with pytest.raises(TypeError):
+        launch_iq3_s_fp8_matmul_grouped(xv, xs, [fields(16, 2), "not prepared"])
+    with pytest.raises(ValueError, match="x_scales"):
+        launch_iq3_s_fp8_matmul_grouped(xv, xs[:, :8], [fields(16, 2)])
     with pytest.raises(RuntimeError, match="no tuned config"):
         select_config(4, 4096, 4096, arch="gfx942")
-    assert select_config(4, 4096, 4096, arch="gfx950")["kernel"] == 1
+    assert select_config(4, 4096, 4096, arch="gfx950")["kernel"] == 0  # the library picks the family
     assert [m_bucket(m) for m in (1, 2, 3, 4, 5, 16, 17, 2048)] == [1, 2, 4, 4, 8, 16, 32, 2048]
+
+
+def test_split_table_is_exact():
+    """(1+2s)(2l+1) = 2*E4M3(hi) + 2*E4M3(lo) for every scale nibble and grid level, hi is
+    the product rounded to 4 significant bits with ties to even, |lo| <= 16."""
+    from fractions import Fraction
+    from mambo_amd import _native
+    from oracle import oracle
+    table = np.zeros(64, dtype=np.uint32)
+    assert _native.lib().mambo_iq3s_split_table(table.ctypes.data) == 0
+    dec = oracle.e4m3_decode_all()  # float value of every E4M3 byte
+
+    def rne4(p):  # nearest value with 4 significant bits, ties to the even one
+        step = 1 << max(0, p.bit_length() - 4)
+        lo, hi = p // step * step, (p // step + 1) * step
+        if p - lo != hi - p:
+            return lo if p - lo < hi - p else hi
+        return lo if (lo // step) % 2 == 0 else hi
+
+    for s in range(16):
+        for lvl in range(8):
+            w = lvl >> 2
+            hb = int(table[4 * s + w] >> (8 * (lvl & 3))) & 0xFF
+            lb = int(table[4 * s + 2 + w] >> (8 * (lvl & 3))) & 0xFF
+            p = (1 + 2 * s) * (2 * lvl + 1)
+            hi, lo = Fraction(float(dec[hb])) * 2, Fraction(float(dec[lb])) * 2
+            assert hb < 0x80 and hi == rne4(p), (s, lvl, hb, hi)
+            assert hi + lo == p and abs(lo) <= 16, (s, lvl, hi, lo)

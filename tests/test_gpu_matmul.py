@@ -197,3 +197,51 @@ def test_graph_capture_replays_match_eager(gpu):
         for o, r in zip(outs, ref):
             torch.testing.assert_close(o, r, rtol=1e-5, atol=1e-5)
         _ = (xq.float().sum()).item()  # eager work between replays
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 33])
+def test_grouped_projections_match_single_launches(gpu, m):
+    """Three projections of one input in one launch (q/k/v-like, ragged N): each output
+    is bit-identical to its own launch under the same configuration and matches the
+    oracle; a K-split grouped launch (zero fill + atomics) matches the oracle too."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    k = 2048
+    raws = [make_synthetic_iq3_s(n, k, seed=40 + i) for i, n in enumerate((100, 37, 64))]
+    fields = [prepare_iq3_s_fields(torch.from_numpy(r).to(gpu)) for r in raws]
+    x = np.random.default_rng(7 + m).standard_normal((m, k)).astype(np.float32)
+    xv, xs = oracle.quantize_mxfp8(x)
+    xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+    expected = [oracle.iq3s_fp8_matmul(xv, xs, r) for r in raws]
+    cfg = {"waves": 2, "split_k": 1}
+    step(f"grouped matmul M={m} N=100+37+64 K=2048 cfg={cfg}")
+    outs = launch_iq3_s_fp8_matmul_grouped(xvg, xsg, fields, config=cfg)
+    singles = [launch_iq3_s_fp8_matmul(xvg, xsg, f, config=cfg) for f in fields]
+    torch.cuda.synchronize()
+    for o, s_, e in zip(outs, singles, expected):
+        np.testing.assert_array_equal(o.cpu().numpy(), s_.cpu().numpy())
+        check(o.cpu().numpy(), e)
+    step(f"grouped matmul M={m} default config and split_k=4")
+    for c in (None, {"waves": 2, "split_k": 4}):
+        outs = launch_iq3_s_fp8_matmul_grouped(xvg, xsg, fields, config=c)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, expected):
+            check(o.cpu().numpy(), e)
+
+
+def test_grouped_into_strided_outputs(gpu):
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul_grouped
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    k, m = 1024, 3
+    raws = [make_synthetic_iq3_s(n, k, seed=60 + n) for n in (20, 33)]
+    fields = [prepare_iq3_s_fields(torch.from_numpy(r).to(gpu)) for r in raws]
+    xv, xs = oracle.quantize_mxfp8(np.random.default_rng(3).standard_normal((m, k)).astype(np.float32))
+    big = torch.full((m, 80), 7.0, dtype=torch.float32, device=gpu)
+    step("grouped matmul into column slices of one buffer")
+    launch_iq3_s_fp8_matmul_grouped(torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu), fields,
+                                    outs=[big[:, 4:24], big[:, 40:73]])
+    torch.cuda.synchronize()
+    b = big.cpu().numpy()
+    check(b[:, 4:24], oracle.iq3s_fp8_matmul(xv, xs, raws[0]))
+    check(b[:, 40:73], oracle.iq3s_fp8_matmul(xv, xs, raws[1]))
+    assert np.all(b[:, :4] == 7.0) and np.all(b[:, 24:40] == 7.0) and np.all(b[:, 73:] == 7.0)
