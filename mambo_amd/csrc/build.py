@@ -28,7 +28,7 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-fPIC",
-    "-std=c++17",
+    "-std=c++20",
     "-munsafe-fp-atomics",
     # Keep hipcc from emitting packed FP32 instructions (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -36,7 +36,7 @@ __constant__ GridTables c_grid = kGridTables;
 // unit E8M0 scales (2^0).
 // Kept in the global address space (not constant) so the activation pointers stay
 // global and the loads are global_load, not flat_load.
-__device__ __align__(16) uint8_t g_zero_chunk[128] = {};
+__device__ __align__(16) uint8_t g_zero_chunk[64] = {};
 __device__ uint8_t g_unit_scales[2] = {127, 127};
 __constant__ SplitTables c_split = kSplitTables;
 
@@ -48,6 +48,10 @@ constexpr int kDepth = MAMBO_STREAM_DEPTH;
 #ifndef MAMBO_SCHED_FENCE
 #define MAMBO_SCHED_FENCE 1
 #endif
+// Accumulation chains of the dense kernel's four MFMAs per block (hi and lo terms).
+#ifndef MAMBO_DENSE_CHAINS
+#define MAMBO_DENSE_CHAINS 2
+#endif
 
 
 struct WTile {
@@ -58,14 +62,15 @@ struct WTile {
     uint16_t dh;  // fp16 d of row col
 };
 
-__device__ __forceinline__ WTile load_w(const uint8_t *__restrict__ tb, int lane, int col)
+// tb is wave-uniform; the lane offsets are 32-bit so the loads use a scalar base.
+__device__ __forceinline__ WTile load_w(const uint8_t *__restrict__ tb, uint32_t lane, uint32_t col)
 {
     WTile w;
-    w.ia = *reinterpret_cast<const uint4 *>(tb + kTileIdxA + 16 * lane);
-    w.ib = *reinterpret_cast<const uint16_t *>(tb + kTileIdxB + 2 * lane);
-    w.sg = *reinterpret_cast<const uint2 *>(tb + kTileSigns + 8 * lane);
+    w.ia = *reinterpret_cast<const uint4 *>(tb + (kTileIdxA + 16u * lane));
+    w.ib = *reinterpret_cast<const uint16_t *>(tb + (kTileIdxB + 2u * lane));
+    w.sg = *reinterpret_cast<const uint2 *>(tb + (kTileSigns + 8u * lane));
     w.sc = tb[kTileScales + lane];
-    w.dh = *reinterpret_cast<const uint16_t *>(tb + kTileD + 2 * col);
+    w.dh = *reinterpret_cast<const uint16_t *>(tb + (kTileD + 2u * col));
     return w;
 }
 
@@ -162,9 +167,10 @@ __device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at
     }
 }
 
-// Dynamic LDS of the stream kernel: codebook (2 KiB), cross-wave partial sums of one
-// 4-row sub-tile [W][4][64] f32, a zero chunk + unit scales for lanes off the block diagonal, and -
-// when kLdsAct - the workgroup's activation rows [rows][K] and scales [rows][K/32].
+// Dynamic LDS of the stream kernel (the codebook sits in static LDS, so its address is a
+// compile-time constant folded into the reads): cross-wave partial sums of one 4-row
+// sub-tile [W][4][64] f32, a zero chunk + unit scales for lanes off the block diagonal,
+// and - when kLdsAct - the workgroup's activation rows [rows][K] and scales [rows][K/32].
 struct StreamLds {
     int red, zero, x, xs, total;
 };
@@ -172,7 +178,7 @@ struct StreamLds {
 __host__ __device__ inline StreamLds stream_lds(int U, int W, int rows, int K, bool lds_act)
 {
     StreamLds l;
-    l.red = 2048;
+    l.red = 0;
     l.zero = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
     (void)U;
     l.x = l.zero + 80;
@@ -228,12 +234,12 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
     const int last = first + (count - 1) * W;
     WTile wr[kDepth];
-    const uint8_t *lut = smem;
+    __shared__ uint32_t s_grid[512];
+    const uint8_t *lut = reinterpret_cast<const uint8_t *>(s_grid);
     {
         const int nt = W * 64;
-        uint32_t *lw = reinterpret_cast<uint32_t *>(smem);
         for (int i = tid; i < 512; i += nt)
-            lw[i] = c_grid.fp8[i];
+            s_grid[i] = c_grid.fp8[i];
         if (tid < 20)
             reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 16 ? 0u : 0x7F7F7F7Fu;
         if constexpr (kLdsAct) {
@@ -404,34 +410,32 @@ struct ADense {
     uint8_t s[2];
 };
 
-struct ALaneD {
-    const uint8_t *x; // this lane's first 16 activation bytes of block 0, MFMA 0
-    const uint8_t *s; // this lane's E8M0 scale of block 0, MFMA 0
-    int xstep;        // 256 or 0
-    int sstep;        // 8 or 0
-};
-
-__device__ __forceinline__ void load_a_dense(ADense &at, const ALaneD &al, int b)
+// Activation bytes and scales of one lane at block b: base + off + 256*b (values) and
+// sbase + soff + 8*b (scales), with wave-uniform bases and 32-bit lane offsets.
+__device__ __forceinline__ void load_a_dense(ADense &at, const uint8_t *__restrict__ xbase, uint32_t xoff,
+                                             const uint8_t *__restrict__ sbase, uint32_t soff, int b)
 {
-    const uint8_t *xp = al.x + b * al.xstep;
-    const uint8_t *sp = al.s + b * al.sstep;
+    const uint8_t *xp = xbase + 256 * (int64_t)b;
+    const uint8_t *sp = sbase + 8 * (int64_t)b;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const uint4 lo = *reinterpret_cast<const uint4 *>(xp + 32 * h);
-        const uint4 hi = *reinterpret_cast<const uint4 *>(xp + 32 * h + 64);
+        const uint4 lo = *reinterpret_cast<const uint4 *>(xp + (xoff + 32u * h));
+        const uint4 hi = *reinterpret_cast<const uint4 *>(xp + (xoff + 32u * h + 64u));
         at.a[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        at.s[h] = sp[h];
+        at.s[h] = sp[soff + h];
     }
 }
 
 // hi and lo words of code C of a group: level bytes select from the split table entry
-// (tab.x/.y: hi of levels 0-3/4-7, tab.z/.w: lo), signs moved onto bits 7,15,23,31.
+// (tab.x/.y: hi of levels 0-3/4-7, tab.z/.w: lo); the four signs, moved onto bits
+// 7,15,23,31 by one shift of the transposed sign word, are OR-ed into hi and XOR-ed into
+// lo (one v_bitop3 each: a | (b & c) = 0xF8, a ^ (b & c) = 0x78).
 template <int C>
 __device__ __forceinline__ void split_word(uint32_t lv, uint32_t p, uint4 tab, int &hi, int &lo)
 {
-    const uint32_t m = funnel_shr(p, p, (25 + C) & 31) & 0x80808080u;
-    hi = (int)(__builtin_amdgcn_perm(tab.y, tab.x, lv) | m);
-    lo = (int)(__builtin_amdgcn_perm(tab.w, tab.z, lv) ^ m);
+    const uint32_t r = funnel_shr(p, p, (25 + C) & 31);
+    hi = (int)__builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(tab.y, tab.x, lv), r, 0x80808080u, 0xF8);
+    lo = (int)__builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(tab.w, tab.z, lv), r, 0x80808080u, 0x78);
 }
 
 template <int H, int... C>
@@ -457,12 +461,12 @@ __device__ __forceinline__ void to_dense_order(v8i &b)
 }
 
 __device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, const uint8_t *lvl,
-                                              const uint8_t *split, float (&acc)[4], bool valid)
+                                              const uint4 *split, float (&acc)[4], bool valid)
 {
     const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
     const uint32_t sc = w.sc;
-    const uint4 t0 = *reinterpret_cast<const uint4 *>(split + 16 * (sc & 15u));
-    const uint4 t1 = *reinterpret_cast<const uint4 *>(split + 16 * (sc >> 4));
+    const uint4 t0 = split[sc & 15u];
+    const uint4 t1 = split[sc >> 4];
     v8i h0, l0, h1, l1;
     decode_split<0>(s, w.sg.x, lvl, t0, h0, l0, std::make_integer_sequence<int, 8>{});
     decode_split<1>(s, w.sg.y, lvl, t1, h1, l1, std::make_integer_sequence<int, 8>{});
@@ -470,33 +474,38 @@ __device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, 
     to_dense_order(l0);
     to_dense_order(h1);
     to_dense_order(l1);
-    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
     // B scale 2^1: the split terms are stored halved
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#if MAMBO_DENSE_CHAINS == 1
+    v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, c, 0, 0, 0, (int)at.s[0], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c, 0, 0, 0, (int)at.s[1], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c, 0, 0, 0, (int)at.s[1], 0, 128);
+#else
     v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
     v4f c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
     c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c1, 0, 0, 0, (int)at.s[1], 0, 128);
     c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c2, 0, 0, 0, (int)at.s[1], 0, 128);
+    const v4f c = c1 + c2;
+#endif
     const float f = valid ? half_bits_to_float((uint16_t)w.dh) : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-        acc[r] = __builtin_fmaf(c1[r] + c2[r], f, acc[r]);
+        acc[r] = __builtin_fmaf(c[r], f, acc[r]);
 }
 
-// LDS of the dense kernel: level grid (2 KiB), split tables (256 B), cross-wave partial
-// sums [W][4][64] f32, 128 zero bytes + unit scales for rows past M (a lane reads up to
-// byte 32 + 64 + 16 of its chunk), and - when kLdsAct -
-// the chunk's activation rows [rows][K] and scales [rows][K/32].
+// Dynamic LDS of the dense kernel (level grid and split tables sit in static LDS):
+// cross-wave partial sums [W][4][64] f32 and - when kLdsAct - the chunk's activation rows
+// [rows][K] and scales [rows][K/32].
 struct DenseLds {
-    int split, red, zero, x, xs, total;
+    int red, x, xs, total;
 };
 
 __host__ __device__ inline DenseLds dense_lds(int W, int rows, int K, bool lds_act)
 {
     DenseLds l;
-    l.split = 2048;
-    l.red = l.split + 256;
-    l.zero = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
-    l.x = l.zero + 144;
+    l.red = 0;
+    l.x = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
     l.xs = l.x + (lds_act ? rows * K : 0);
     l.total = l.xs + (lds_act ? rows * (K / 32) : 0);
     return l;
@@ -508,6 +517,8 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                                                             GroupArgs ga, int B, int bps, int atomic)
 {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t s_lvl[512];
+    __shared__ uint4 s_split[16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = B * 256;
@@ -535,13 +546,10 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     const int last = first + (count - 1) * W;
     {
         const int nt = W * 64;
-        uint32_t *lw = reinterpret_cast<uint32_t *>(smem);
         for (int i = tid; i < 512; i += nt)
-            lw[i] = c_grid.level[i];
-        if (tid < 64)
-            reinterpret_cast<uint32_t *>(smem + L.split)[tid] = c_split.w[tid >> 2][tid & 3];
-        if (tid < 36)
-            reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 32 ? 0u : 0x7F7F7F7Fu;
+            s_lvl[i] = c_grid.level[i];
+        if (tid < 16)
+            s_split[tid] = uint4{c_split.w[tid][0], c_split.w[tid][1], c_split.w[tid][2], c_split.w[tid][3]};
         if constexpr (kLdsAct) {
             const int nx = rows * K / 16;
             for (int c = tid; c < nx; c += nt) {
@@ -557,25 +565,25 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         }
     }
     __syncthreads();
-    const uint8_t *lvl = smem;
-    const uint8_t *split = smem + L.split;
+    const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
 
-    // A lane: token col of the chunk; bytes of group 4*(q>>1) + h, half q&1 (+64 for the
-    // second 16 bytes); scale of group 4*(q&1) + 2*(q>>1) + h.
-    ALaneD al;
-    {
-        const bool on = col < rows;
-        const int xoff = 32 * (4 * (q >> 1)) + 16 * (q & 1);
-        const int soff = 4 * (q & 1) + 2 * (q >> 1);
-        if constexpr (kLdsAct) {
-            al.x = on ? smem + L.x + col * K + xoff : smem + L.zero;
-            al.s = on ? smem + L.xs + col * (K / 32) + soff : smem + L.zero + 128;
-        } else {
-            al.x = on ? xv + (m0 + col) * ldxv + xoff : g_zero_chunk;
-            al.s = on ? xs + (m0 + col) * ldxs + soff : g_unit_scales;
-        }
-        al.xstep = on ? 256 : 0;
-        al.sstep = on ? 8 : 0;
+    // A lane: token col of the chunk, bytes of group 4*(q>>1) + h, half q&1 (+64 bytes for
+    // group 4*(q>>1) + 2 + h), scale of group 4*(q&1) + 2*(q>>1) + h. Lanes of tokens past
+    // M read the chunk's last token: they only feed output rows that are never stored.
+    const int rowc = min(col, rows - 1);
+    const uint32_t xo = 32u * (4 * (q >> 1)) + 16u * (q & 1), so = 4u * (q & 1) + 2u * (q >> 1);
+    const uint8_t *xbase, *sbase;
+    uint32_t xoff, soff;
+    if constexpr (kLdsAct) {
+        xbase = smem + L.x;
+        sbase = smem + L.xs;
+        xoff = (uint32_t)(rowc * K) + xo;
+        soff = (uint32_t)(rowc * (K / 32)) + so;
+    } else {
+        xbase = xv + m0 * ldxv;
+        sbase = xs + m0 * ldxs;
+        xoff = (uint32_t)(rowc * ldxv) + xo;
+        soff = (uint32_t)(rowc * ldxs) + so;
     }
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -586,7 +594,7 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         for (int j = 0; j < kDepth - 1; ++j) {
             wr[j] = load_w(wt + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
-                load_a_dense(ar[j], al, min(first + j * W, last));
+                load_a_dense(ar[j], xbase, xoff, sbase, soff, min(first + j * W, last));
         }
         for (int i0 = 0; i0 < count; i0 += kDepth) {
 #pragma unroll
@@ -596,14 +604,14 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                 const int bp = min(first + (i + kDepth - 1) * W, last);
                 wr[slot] = load_w(wt + (int64_t)bp * kTileBytes, lane, col);
                 if constexpr (!kLdsAct)
-                    load_a_dense(ar[slot], al, bp);
+                    load_a_dense(ar[slot], xbase, xoff, sbase, soff, bp);
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
                 if constexpr (kLdsAct) {
-                    load_a_dense(ar[0], al, min(first + i * W, last));
-                    compute_dense(wr[j], ar[0], lvl, split, acc, i < count);
+                    load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
+                    compute_dense(wr[j], ar[0], lvl, s_split, acc, i < count);
                 } else {
-                    compute_dense(wr[j], ar[j], lvl, split, acc, i < count);
+                    compute_dense(wr[j], ar[j], lvl, s_split, acc, i < count);
                 }
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
@@ -642,6 +650,215 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                 *o = acc[r];
         }
     }
+}
+
+// ============================================================================ tiled kernel
+// Large M (prefill). A workgroup of W waves computes a 16*MT (tokens) x 16*NT*W (weight
+// rows) output tile over all of K. Per 256-weight block the activations of the tile's
+// tokens (16*MT rows x 256 bytes + 8 E8M0 scales each) are staged in LDS, double
+// buffered, with a 272-byte row pitch so the 16 rows read by one lane group start in
+// different LDS banks. Each wave decodes its NT weight tiles once per block into dense
+// hi/lo operands (as the dense kernel does) and reuses them for all MT token sub-tiles:
+// MT*NT*4 MFMAs per block and wave, the fp16 d applied per block in f32. The grid's x
+// runs over weight-row tiles (grouped projections start on a workgroup boundary), y
+// over token tiles.
+
+constexpr int kTiledPitch = 272;
+
+__host__ __device__ constexpr int tiled_lds_bytes(int MT)
+{
+    return 2 * (16 * MT * kTiledPitch + 16 * MT * 8);
+}
+
+template <int MT, int NT, int W>
+__global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+                                                            const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
+                                                            GroupArgs ga, int B)
+{
+    constexpr int kRows = 16 * MT;
+    constexpr int kABytes = kRows * kTiledPitch;
+    constexpr int kSBytes = kRows * 8;
+    constexpr int kThreads = W * 64;
+    constexpr int kChunks = kRows * 16;                     // 16-byte chunks of one A block
+    constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
+    extern __shared__ __align__(16) uint8_t smem[];          // A[2][kABytes], S[2][kSBytes]
+    __shared__ uint32_t s_lvl[512];
+    __shared__ uint4 s_split[16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, q = lane >> 4;
+
+    // this workgroup's projection; tile_begin counts workgroups here
+    const uint8_t *packed = ga.packed[0];
+    float *out = ga.out[0];
+    int64_t N = ga.n[0], ldo = ga.ldo[0], wg = blockIdx.x;
+#pragma unroll
+    for (int g = 1; g < kMaxGroup; ++g)
+        if (g < ga.count && (int64_t)blockIdx.x >= ga.tile_begin[g]) {
+            packed = ga.packed[g];
+            out = ga.out[g];
+            N = ga.n[g];
+            ldo = ga.ldo[g];
+            wg = blockIdx.x - ga.tile_begin[g];
+        }
+    const int64_t tiles = (N + kTileRows - 1) / kTileRows;
+    const int64_t m0 = (int64_t)blockIdx.y * kRows;
+    // weight tiles of this wave (clamped to the last tile; stores are masked)
+    const uint8_t *wt[NT];
+    int64_t tile[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        tile[nt] = wg * (NT * W) + wave * NT + nt;
+        wt[nt] = packed + min(tile[nt], tiles - 1) * (int64_t)B * kTileBytes;
+    }
+
+    for (int i = tid; i < 512; i += kThreads)
+        s_lvl[i] = c_grid.level[i];
+    if (tid < 16)
+        s_split[tid] = uint4{c_split.w[tid][0], c_split.w[tid][1], c_split.w[tid][2], c_split.w[tid][3]};
+
+    // A staging: chunk c of block b = row c >> 4 (clamped to M-1), bytes 16*(c & 15);
+    // thread tid owns chunks tid + j*kThreads.
+    uint4 stage[kPerThread];
+    uint2 sstage = {0u, 0u};
+    const uint8_t *xtile = xv + m0 * ldxv; // chunk rows past M are clamped to row M-1
+    const int64_t last_row = M - 1 - m0;
+    // scales: thread tid stages row min(tid, kRows-1); the threads past kRows rewrite the
+    // last row's identical bytes, which keeps the staging branch-free
+    const int srow_ = min(tid, kRows - 1);
+    const uint8_t *ssrc = xs + min(m0 + srow_, M - 1) * ldxs;
+    // (fold expressions over an index sequence: every staging register has a
+    // compile-time index, so the array stays in registers across iterations)
+    constexpr auto kJ = std::make_integer_sequence<int, kPerThread>{};
+    auto load_one = [&](int j, int b) -> uint4 {
+        const int c = min(tid + j * kThreads, kChunks - 1);
+        return *reinterpret_cast<const uint4 *>(xtile + min<int64_t>(c >> 4, last_row) * ldxv +
+                                                (256 * (int64_t)b + 16 * (c & 15)));
+    };
+    auto store_one = [&](int j, int buf, uint4 v) {
+        const int c = tid + j * kThreads;
+        if (kChunks % kThreads == 0 || c < kChunks)
+            *reinterpret_cast<uint4 *>(smem + buf * kABytes + (c >> 4) * kTiledPitch + 16 * (c & 15)) = v;
+    };
+#define MAMBO_LOAD_STAGE(b)                                                                                        \
+    do {                                                                                                           \
+        [&]<int... J>(std::integer_sequence<int, J...>) { ((stage[J] = load_one(J, (b))), ...); }(kJ);             \
+        sstage = *reinterpret_cast<const uint2 *>(ssrc + 8 * (int64_t)(b));                                        \
+    } while (0)
+#define MAMBO_STORE_STAGE(buf)                                                                                     \
+    do {                                                                                                           \
+        [&]<int... J>(std::integer_sequence<int, J...>) { (store_one(J, (buf), stage[J]), ...); }(kJ);             \
+        *reinterpret_cast<uint2 *>(smem + 2 * kABytes + (buf) * kSBytes + 8 * srow_) = sstage;                     \
+    } while (0)
+
+    // A operand offsets of this lane inside a staged block (token row col of each
+    // sub-tile; see the dense kernel for the byte and scale order)
+    const uint32_t xo = 32u * (4 * (q >> 1)) + 16u * (q & 1), so = 4u * (q & 1) + 2u * (q >> 1);
+
+    float acc[MT][NT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mt][nt][r] = 0.0f;
+
+    // Pipeline: in iteration b the staging registers hold block b+1 (loaded one iteration
+    // earlier) and are written to LDS at the top, then refilled with block b+2; the
+    // loads are consumed only in the next iteration, so they overlap a whole block of
+    // math and cannot be moved down to their stores.
+    WTile wcur[NT], wnext[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+        wcur[nt] = load_w(wt[nt], lane, col);
+    MAMBO_LOAD_STAGE(0);
+    MAMBO_STORE_STAGE(0);
+    MAMBO_LOAD_STAGE(min(1, B - 1));
+    __syncthreads();
+
+    for (int b = 0; b < B; ++b) {
+        // buffer (b+1)&1 was last read in block b-1, before the previous barrier; after
+        // the last block this fills the idle buffer
+        MAMBO_STORE_STAGE((b + 1) & 1);
+        MAMBO_LOAD_STAGE(min(b + 2, B - 1));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+            wnext[nt] = load_w(wt[nt] + (int64_t)min(b + 1, B - 1) * kTileBytes, lane, col);
+        __builtin_amdgcn_sched_barrier(0);
+
+        v8i bh[NT][2], bl[NT][2];
+        float d[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const WTile &w = wcur[nt];
+            const uint32_t s5[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
+            const uint4 t0 = s_split[w.sc & 15u], t1 = s_split[(uint32_t)w.sc >> 4];
+            const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
+            decode_split<0>(s5, w.sg.x, lvl, t0, bh[nt][0], bl[nt][0], std::make_integer_sequence<int, 8>{});
+            decode_split<1>(s5, w.sg.y, lvl, t1, bh[nt][1], bl[nt][1], std::make_integer_sequence<int, 8>{});
+            to_dense_order(bh[nt][0]);
+            to_dense_order(bl[nt][0]);
+            to_dense_order(bh[nt][1]);
+            to_dense_order(bl[nt][1]);
+            d[nt] = half_bits_to_float((uint16_t)w.dh);
+        }
+        const uint8_t *a = smem + (b & 1) * kABytes;
+        const uint8_t *sa = smem + 2 * kABytes + (b & 1) * kSBytes;
+        // A fragments read per sub-tile (the other resident wave of the SIMD covers the LDS
+        // latency); the fence per sub-tile keeps the compiler from hoisting every LDS
+        // read of the block into registers.
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint8_t *ar = a + (16 * mt + col) * kTiledPitch + xo;
+            const uint8_t *sr = sa + (16 * mt + col) * 8 + so;
+            v8i av[2];
+            int sc[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint4 lo = *reinterpret_cast<const uint4 *>(ar + 32 * h);
+                const uint4 hi = *reinterpret_cast<const uint4 *>(ar + 32 * h + 64);
+                av[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                sc[h] = sr[h];
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bh[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
+                v4f c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bl[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
+                c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bh[nt][1], c1, 0, 0, 0, sc[1], 0, 128);
+                c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bl[nt][1], c2, 0, 0, 0, sc[1], 0, 128);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[mt][nt][r] = __builtin_fmaf(c1[r] + c2[r], d[nt], acc[mt][nt][r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+            wcur[nt] = wnext[nt];
+        __syncthreads();
+    }
+
+    // D[i][j] of sub-tile (mt, nt): lane j + 16*(i/4), register i%4 -> token
+    // m0 + 16*mt + 4q + r, weight row 16*tile + col.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int64_t n = tile[nt] * kTileRows + col;
+        if (n >= N)
+            continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + 16 * mt + 4 * q + r;
+                if (m < M)
+                    out[m * ldo + n] = acc[mt][nt][r];
+            }
+    }
+#undef MAMBO_LOAD_STAGE
+#undef MAMBO_STORE_STAGE
 }
 
 __global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t cols, int64_t ld)
@@ -719,6 +936,30 @@ int launch_dense(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t str
     return MAMBO_OK;
 }
 
+template <int MT, int NT, int W>
+void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
+                    int64_t M, const GroupArgs &ga, int B)
+{
+    hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv, ldxv, xs,
+                       ldxs, M, ga, B);
+}
+
+// Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves).
+int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                 const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B)
+{
+#define MAMBO_T(A, C, D)                                                                                           \
+    if (mt == A && nt == C && waves == D) {                                                                        \
+        launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B);                                       \
+        return MAMBO_OK;                                                                                           \
+    }
+    MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
+    MAMBO_T(4, 2, 8) MAMBO_T(4, 2, 4) MAMBO_T(4, 1, 8) MAMBO_T(4, 1, 4)
+#undef MAMBO_T
+    return mambo_fail(MAMBO_ERR_VALUE, "tiled kernel: no build for tile_m=%d, tile_n=%d, waves=%d", 16 * mt,
+                      16 * nt * waves, waves);
+}
+
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Waves the default configuration aims for: about two rounds of 4 resident waves per
@@ -728,6 +969,13 @@ constexpr int64_t kTargetWaves = 8192;
 constexpr int64_t kMinWaves = 512;
 // Activations are staged in LDS when the workgroup's rows take at most this much.
 constexpr int kMaxLdsAct = 40 * 1024;
+// Compute units of an MI355X (the tiled default sizes its grid to at least one
+// workgroup per CU).
+constexpr int64_t kCUs = 256;
+// Token count from which the default configuration uses the tiled kernel.
+constexpr int64_t kTiledMinM = 64;
+// Dynamic LDS per workgroup (the static codebook tables add 2.3 KiB).
+constexpr int kMaxDynLds = 60 * 1024;
 
 bool valid_waves(int w)
 {
@@ -747,7 +995,28 @@ extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, m
     // Block-diagonal activations cost nothing extra while one MFMA covers every token
     // (M <= 4); beyond that the dense kernel does 4 MFMAs per block for 16 tokens where
     // the block-diagonal one needs 2 per 4 tokens and an activation sub-tile each.
-    c.kernel = m <= 4 ? MAMBO_GEMM_STREAM : MAMBO_GEMM_DENSE;
+    c.kernel = m <= 4 ? MAMBO_GEMM_STREAM : m < kTiledMinM ? MAMBO_GEMM_DENSE : MAMBO_GEMM_TILED;
+    if (c.kernel == MAMBO_GEMM_TILED) {
+        // The largest tile that still gives every CU a workgroup (measured on gfx950:
+        // 128 tokens x 256 weight rows x 8 waves is fastest when the grid fills the chip;
+        // 64 x 128 x 8, then 64 x 64 x 4, for small N x M).
+        const int64_t rt = cdiv(n, kTileRows);
+        c.split_k = 1;
+        c.waves = 8;
+        if (cdiv(rt, 16) * cdiv(m, 128) >= kCUs) {
+            c.tile_m = 128;
+            c.tile_n = 256;
+        } else if (cdiv(rt, 8) * cdiv(m, 64) >= kCUs) {
+            c.tile_m = 64;
+            c.tile_n = 128;
+        } else {
+            c.tile_m = 64;
+            c.tile_n = 64;
+            c.waves = 4;
+        }
+        *out = c;
+        return MAMBO_OK;
+    }
     const int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
     // Waves per workgroup: the largest power of two up to 8 (16 for M <= 4 and grids of at
     // most 2K waves; wider sub-tiles spill at 1024 threads) that divides the K blocks evenly, keeps at least two blocks per wave and at
@@ -775,8 +1044,17 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
 {
     MAMBO_REQUIRE(cfg != nullptr, MAMBO_ERR_VALUE, "cfg must not be NULL");
     MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
-    MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM || cfg->kernel == MAMBO_GEMM_DENSE, MAMBO_ERR_VALUE,
-                  "unsupported kernel family %d", cfg->kernel);
+    MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM || cfg->kernel == MAMBO_GEMM_DENSE ||
+                      cfg->kernel == MAMBO_GEMM_TILED,
+                  MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
+    if (cfg->kernel == MAMBO_GEMM_TILED) {
+        MAMBO_REQUIRE(cfg->tile_m == 64 || cfg->tile_m == 128, MAMBO_ERR_VALUE, "tiled: tile_m must be 64 or 128");
+        MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE, "tiled: waves must be 4 or 8");
+        MAMBO_REQUIRE(cfg->tile_n == 16 * cfg->waves || cfg->tile_n == 32 * cfg->waves, MAMBO_ERR_VALUE,
+                      "tiled: tile_n must be 16 or 32 weight rows per wave");
+        MAMBO_REQUIRE(cfg->split_k == 1, MAMBO_ERR_VALUE, "tiled: split_k must be 1");
+        return MAMBO_OK;
+    }
     MAMBO_REQUIRE(valid_waves(cfg->waves), MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16");
     MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                   "split_k must be in [1, K/256]");
@@ -797,6 +1075,7 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     MAMBO_REQUIRE(blocks <= (1 << 20), MAMBO_ERR_VALUE, "K too large");
     const int64_t k = blocks * 256;
     MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32, MAMBO_ERR_VALUE, "activation row strides must cover the row");
+    MAMBO_REQUIRE(ldxv < ((int64_t)1 << 27), MAMBO_ERR_VALUE, "activation row stride too large");
     MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
                   "x_values base and row stride must be 16-byte aligned");
     GroupArgs ga = {};
@@ -836,6 +1115,25 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         if (rc)
             return rc;
     }
+    if (c.kernel == MAMBO_GEMM_TILED) {
+        const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);
+        MAMBO_REQUIRE((uintptr_t)xs % 8 == 0 && ldxs % 8 == 0, MAMBO_ERR_VALUE,
+                      "tiled: x_scales base and row stride must be 8-byte aligned");
+        // workgroups per projection; tile_begin counts workgroups for this kernel
+        GroupArgs gt = ga;
+        int64_t wgs = 0;
+        for (int g = 0; g < count; ++g) {
+            gt.tile_begin[g] = wgs;
+            wgs += cdiv(cdiv(ga.n[g], kTileRows), (int64_t)nt * c.waves);
+        }
+        const int64_t mtiles = cdiv(m, c.tile_m);
+        MAMBO_REQUIRE(wgs <= 0x7FFFFFFF && mtiles <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
+        rc = launch_tiled(mt, nt, c.waves, dim3((unsigned)wgs, (unsigned)mtiles), s, xv, ldxv, xs, ldxs, m, gt,
+                          (int)blocks);
+        if (rc)
+            return rc;
+        return mambo_check_launch("iq3s_fp8_matmul (tiled)");
+    }
     const int64_t mchunks = cdiv(m, 16);
     MAMBO_REQUIRE(tiles <= 0x7FFFFFFF && mchunks <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
     const int bps = (int)cdiv(blocks, c.split_k);
@@ -858,16 +1156,16 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
     const int B = (int)blocks;
     if (c.kernel == MAMBO_GEMM_DENSE) {
-        if (lds_act && dense_lds(c.waves, rows, (int)k, true).total > 64 * 1024)
+        if (lds_act && dense_lds(c.waves, rows, (int)k, true).total > kMaxDynLds)
             lds_act = false;
         const DenseLds L = dense_lds(c.waves, rows, (int)k, lds_act);
         rc = launch_dense(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic);
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
-        if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > 64 * 1024)
+        if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > kMaxDynLds)
             lds_act = false;
         const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
-        MAMBO_REQUIRE(L.total <= 64 * 1024, MAMBO_ERR_VALUE,
+        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
                       "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
                       c.waves, (long long)m);
         switch (U) {

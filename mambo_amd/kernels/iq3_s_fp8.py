@@ -241,8 +241,9 @@ def launch_iq3_s_fp8_matmul_grouped(x_values: torch.Tensor, x_scales: torch.Tens
 
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
-    search spaces of iq3_s_fp8.py:416-459): kernel family (block-diagonal or dense
-    activations) x waves per workgroup x K split."""
+    search spaces of iq3_s_fp8.py:416-459): stream kernels (block-diagonal or dense
+    activations) x waves per workgroup x K split, and for M >= 32 the tiled kernel's
+    tile shapes."""
     blocks = k // IQ3_S_BLOCK_VALUES
     u = min(4, -(-m // 4))
     space = []
@@ -253,6 +254,12 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
             for split in (1, 2, 4, 8):
                 if split <= blocks // waves:
                     space.append({"kernel": kernel, "waves": waves, "split_k": split})
+    if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup
+        for tile_m in (64, 128):
+            for waves in (4, 8):
+                for rows_per_wave in (16, 32):
+                    space.append({"kernel": _native.GEMM_TILED, "waves": waves, "split_k": 1, "tile_m": tile_m,
+                                  "tile_n": rows_per_wave * waves})
     return space
 
 
@@ -279,7 +286,7 @@ def make_benchmark_cases(iq3_weight: torch.Tensor, tokens: tuple[int, ...] = (4,
 
         return BenchmarkCase(name=f"M={m} N={n_rows} K={k}", stream=stream, launch=launch,
                              search_space=gemm_search_space(m, n_rows, k),
-                             summary_keys=("kernel", "waves", "split_k"),
+                             summary_keys=("kernel", "waves", "split_k", "tile_m", "tile_n"),
                              key=tuned_key(n_rows, k, m))
 
     return [make_case(m) for m in tokens]

@@ -74,12 +74,21 @@ def test_gemm_config_defaults_and_validation():
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(ok)) == 0
     bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 8, "split_k": 1})
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
-    # block-diagonal activations up to M=4, dense beyond
+    ok = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 128,
+                                       "tile_n": 128})
+    assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(ok)) == 0
+    for bad_fields in ({"tile_m": 96}, {"waves": 2, "tile_n": 32}, {"tile_n": 96}, {"split_k": 2}):
+        bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 128,
+                                            "tile_n": 128, **bad_fields})
+        assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE, bad_fields
+    # block-diagonal activations up to M=4, dense up to 63, tiled from 64
     for m, kernel in ((1, _native.GEMM_STREAM), (4, _native.GEMM_STREAM), (5, _native.GEMM_DENSE),
-                      (16, _native.GEMM_DENSE), (2048, _native.GEMM_DENSE)):
+                      (16, _native.GEMM_DENSE), (63, _native.GEMM_DENSE), (64, _native.GEMM_TILED),
+                      (2048, _native.GEMM_TILED)):
         c = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(m, 4096, 16, ctypes.byref(c)) == 0
         assert c.kernel == kernel, (m, c.as_dict())
+        assert lib.mambo_gemm_check_config(m, 4096, 16, ctypes.byref(c)) == 0
 
 
 def test_codebook_exports_match_python_tables():

@@ -76,7 +76,7 @@ def test_every_search_space_config_agrees(gpu):
     n_rows, k = 100, 2048
     raw = make_synthetic_iq3_s(n_rows, k, seed=17)
     fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
-    for m in (1, 6, 16):
+    for m in (1, 6, 16, 37):
         x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
         xv, xs = oracle.quantize_mxfp8(x)
         expected = oracle.iq3s_fp8_matmul(xv, xs, raw)
@@ -199,7 +199,7 @@ def test_graph_capture_replays_match_eager(gpu):
         _ = (xq.float().sum()).item()  # eager work between replays
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 33])
+@pytest.mark.parametrize("m", [1, 5, 16, 33, 130])
 def test_grouped_projections_match_single_launches(gpu, m):
     """Three projections of one input in one launch (q/k/v-like, ragged N): each output
     is bit-identical to its own launch under the same configuration and matches the
@@ -213,7 +213,9 @@ def test_grouped_projections_match_single_launches(gpu, m):
     xv, xs = oracle.quantize_mxfp8(x)
     xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
     expected = [oracle.iq3s_fp8_matmul(xv, xs, r) for r in raws]
-    cfg = {"waves": 2, "split_k": 1}
+    from mambo_amd import _native
+    cfg = {"kernel": _native.GEMM_DENSE, "waves": 2, "split_k": 1} if m < 64 else \
+        {"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 64, "tile_n": 64}
     step(f"grouped matmul M={m} N=100+37+64 K=2048 cfg={cfg}")
     outs = launch_iq3_s_fp8_matmul_grouped(xvg, xsg, fields, config=cfg)
     singles = [launch_iq3_s_fp8_matmul(xvg, xsg, f, config=cfg) for f in fields]
@@ -222,7 +224,7 @@ def test_grouped_projections_match_single_launches(gpu, m):
         np.testing.assert_array_equal(o.cpu().numpy(), s_.cpu().numpy())
         check(o.cpu().numpy(), e)
     step(f"grouped matmul M={m} default config and split_k=4")
-    for c in (None, {"waves": 2, "split_k": 4}):
+    for c in (None, {"kernel": _native.GEMM_DENSE, "waves": 2, "split_k": 4}):
         outs = launch_iq3_s_fp8_matmul_grouped(xvg, xsg, fields, config=c)
         torch.cuda.synchronize()
         for o, e in zip(outs, expected):
@@ -245,3 +247,48 @@ def test_grouped_into_strided_outputs(gpu):
     check(b[:, 4:24], oracle.iq3s_fp8_matmul(xv, xs, raws[0]))
     check(b[:, 40:73], oracle.iq3s_fp8_matmul(xv, xs, raws[1]))
     assert np.all(b[:, :4] == 7.0) and np.all(b[:, 24:40] == 7.0) and np.all(b[:, 73:] == 7.0)
+
+
+@pytest.mark.parametrize("m", [64, 100, 128, 257])
+def test_tiled_kernel_every_tile_shape(gpu, m):
+    """The tiled (prefill) kernel at ragged M and N (N=100: a partial weight tile and
+    partial workgroups), every tile shape it is built for, against the oracle."""
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n_rows, k = 100, 1024
+    raw = make_synthetic_iq3_s(n_rows, k, seed=70 + m)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    x = np.random.default_rng(90 + m).standard_normal((m, k)).astype(np.float32)
+    xv, xs = oracle.quantize_mxfp8(x)
+    expected = oracle.iq3s_fp8_matmul(xv, xs, raw, threads=oracle.default_threads())
+    xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+    for tile_m in (64, 128):
+        for waves in (4, 8):
+            for rows_per_wave in (16, 32):
+                cfg = {"kernel": _native.GEMM_TILED, "waves": waves, "split_k": 1, "tile_m": tile_m,
+                       "tile_n": rows_per_wave * waves}
+                step(f"tiled M={m} N=100 K=1024 cfg={cfg}")
+                out = launch_iq3_s_fp8_matmul(xvg, xsg, fields, config=cfg)
+                torch.cuda.synchronize()
+                check(out.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (4096, 14336)])
+def test_prefill_shape_sampled(gpu, n, k):
+    """M=2048 prefill on 8B shapes (default config: the tiled kernel), sampled output
+    columns against the oracle."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    m = 2048
+    step(f"synth weight {n}x{k}")
+    fields = _synth_weight(gpu, n, k, seed=3)
+    step(f"quantize + matmul M={m} {n}x{k}")
+    xq, xs = launch_quantize_fp8(_synth_act(gpu, m, k, seed=4))
+    out = launch_iq3_s_fp8_matmul(xq, xs, fields).cpu().numpy()
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(n + k).choice(n, 48, replace=False))
+    raw = np.concatenate([oracle.gen_iq3s(3, 1, k // 256, row0=int(r)) for r in rows])
+    expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
+    check(out[:, rows], expected, elementwise=False)
+    assert np.all(np.isfinite(out))
