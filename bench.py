@@ -14,9 +14,11 @@ matmul alone, iq3_s_fp8.py:402-465). --workload llama8b runs the same sweep over
 value = algorithmic bytes per step / step time, with
   bytes per projection = N*K*110/256 (IQ3_S weights) + M*K*33/32 (E4M3 + E8M0 activations)
                          + 4*M*N (f32 output)
-roofline: HBM (8 TB/s) for the weight stream. cpu_baseline: the oracle's restatement of
-the reference CPU path (ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot) on
-its CPU case, one IQ3_S linear N=K=4096 with M=8, timed on this host.
+roofline: HBM (8 TB/s) for the weight stream; for M >= 128 (prefill, MFMA-bound) the
+line reports TFLOP/s (2*M*N*K per projection) against the 5.0 PFLOP/s dense MX-FP8 MFMA
+peak instead. cpu_baseline: the oracle's restatement of the reference CPU path
+(ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot) on its CPU case, one IQ3_S
+linear N=K=4096 with M=8, timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant|copy]
                     [--layers L] [--no-group] [--no-graph]
@@ -35,7 +37,8 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
-MXFP8_PEAK_TFLOPS = 5000.0
+MXFP8_PEAK_TFLOPS = 5000.0  # dense MX-FP8 MFMA peak of MI355X
+PREFILL_M = 128  # from this many tokens the projections are MFMA-bound: report TFLOP/s
 
 LLAMA70B_LAYER = [("q", 8192, 8192, 0), ("k", 1024, 8192, 0), ("v", 1024, 8192, 0), ("o", 8192, 8192, 1),
                   ("gate", 28672, 8192, 2), ("up", 28672, 8192, 2), ("down", 8192, 28672, 3)]
@@ -178,10 +181,11 @@ def run_gemm(args):
     }
 
 
-def cpu_baseline(seconds: float) -> dict:
+def cpu_baseline(seconds: float, unit: str = "GB/s") -> dict:
     """Oracle restatement of the reference CPU path on its CPU case: one IQ3_S linear
     N=K=4096 (seed-0 counter-based blocks), M=8 bf16 ~N(0,1) activations quantized to
-    MXFP8, IQ3_S to_float + float64-accumulated dot per output (all host cores)."""
+    MXFP8, IQ3_S to_float + float64-accumulated dot per output (all host cores).
+    Reported in the unit of the GPU line (GB/s of algorithmic bytes, or TFLOP/s)."""
     import numpy as np
     from oracle import oracle
     n = k = 4096
@@ -196,8 +200,8 @@ def cpu_baseline(seconds: float) -> dict:
         if time.perf_counter() - t0 >= seconds:
             break
     per = (time.perf_counter() - t0) / iters
-    gbs = proj_bytes(m, n, k) / per / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    value = 2 * m * n * k / per / 1e12 if unit == "TFLOP/s" else proj_bytes(m, n, k) / per / 1e9
+    return {"value": round(value, 6), "unit": unit, "cores": threads, "kind": "port",
             "sample": f"one IQ3_S linear N=K=4096, M=8 (the reference CPU case): {iters} runs in {per * iters:.1f} s "
                       f"({per * 1e3:.1f} ms each) of the oracle's to_float + f64-dot restatement "
                       f"of ggml_reference.cpp:495-523 on {threads} threads"}
@@ -315,7 +319,8 @@ def main(argv=None) -> int:
         config = {"workload": workload, "m": 4096, "k": 4096}
     else:
         r = run_gemm(args)
-        metric = "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline"
+        metric = ("fused IQ3_S x MXFP8 GEMM TFLOP/s vs MX-FP8 MFMA roofline" if args.m >= PREFILL_M else
+                  "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline")
         grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
         if args.workload == "llama70b":
             workload = f"llama3-70b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
@@ -324,11 +329,23 @@ def main(argv=None) -> int:
         config = {"workload": workload, "m": args.m, "projections_per_step": r["projections"],
                   "launches_per_step": r["launches"], "weight_gb": round(r["weight_bytes"] / 1e9, 3),
                   "tflops": round(r["tflops"], 3), "graph": not args.no_graph}
-    value = r["value"]
+    mfma_bound = args.workload in ("llama70b", "llama8b") and args.m >= PREFILL_M
+    value = r["tflops"] if mfma_bound else r["value"]
+    unit = "TFLOP/s" if mfma_bound else "GB/s"
+    if mfma_bound:
+        roofline = {"bound": "mfma", "achieved": round(value, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(value / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic(workload),
+                    "algorithmic_flops_per_launch": round(r["step_flops"] / r["launches"]),
+                    "avg_launch_us": round(r["per_launch_us"], 3)}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
+                    "algorithmic_bytes_per_launch": round(r["per_launch_bytes"]),
+                    "avg_launch_us": round(r["per_launch_us"], 3)}
     line = {
         "metric": metric,
         "value": round(value, 2),
-        "unit": "GB/s",
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -339,14 +356,11 @@ def main(argv=None) -> int:
         "dtype": "fp8-e4m3 x iq3_s, f32 accumulate",
         "data": "synthetic (counter-based IQ3_S blocks, bf16 ~N(0,1) activations)",
         "config": config,
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
-                     "algorithmic_bytes_per_launch": round(r["per_launch_bytes"]),
-                     "avg_launch_us": round(r["per_launch_us"], 3)},
+        "roofline": roofline,
     }
     if rank == 0 and not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, unit)
     if rank == 0:
         print(json.dumps(line), flush=True)
     return 0
