@@ -495,23 +495,26 @@ __device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, 
 }
 
 // Dynamic LDS of the dense kernel (level grid and split tables sit in static LDS):
-// cross-wave partial sums [W][4][64] f32 and - when kLdsAct - the chunk's activation rows
-// [rows][K] and scales [rows][K/32].
+// cross-wave partial sums [W][NT][4][64] f32 and - when kLdsAct - the chunk's activation
+// rows [rows][K] and scales [rows][K/32].
 struct DenseLds {
     int red, x, xs, total;
 };
 
-__host__ __device__ inline DenseLds dense_lds(int W, int rows, int K, bool lds_act)
+__host__ __device__ inline DenseLds dense_lds(int W, int NT, int rows, int K, bool lds_act)
 {
     DenseLds l;
     l.red = 0;
-    l.x = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
+    l.x = l.red + (W > 1 ? W * NT * 4 * 64 * 4 : 0);
     l.xs = l.x + (lds_act ? rows * K : 0);
     l.total = l.xs + (lds_act ? rows * (K / 32) : 0);
     return l;
 }
 
-template <int W, bool kLdsAct>
+// A workgroup covers NT weight tiles (16*NT rows); each wave applies one activation
+// fragment per block to all NT tiles, so activation loads per weight byte drop by NT.
+// Grouped projections start on a workgroup boundary (tile_begin counts workgroups).
+template <int W, int NT, bool kLdsAct>
 __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
@@ -524,10 +527,10 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     const int K = B * 256;
     const int64_t m0 = (int64_t)blockIdx.z * 16;
     const int rows = (int)min<int64_t>(16, M - m0);
-    const DenseLds L = dense_lds(W, rows, K, kLdsAct);
+    const DenseLds L = dense_lds(W, NT, rows, K, kLdsAct);
     const uint8_t *packed = ga.packed[0];
     float *out = ga.out[0];
-    int64_t N = ga.n[0], ldo = ga.ldo[0], t = blockIdx.x;
+    int64_t N = ga.n[0], ldo = ga.ldo[0], wg = blockIdx.x;
 #pragma unroll
     for (int g = 1; g < kMaxGroup; ++g)
         if (g < ga.count && (int64_t)blockIdx.x >= ga.tile_begin[g]) {
@@ -535,30 +538,34 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
             out = ga.out[g];
             N = ga.n[g];
             ldo = ga.ldo[g];
-            t = blockIdx.x - ga.tile_begin[g];
+            wg = blockIdx.x - ga.tile_begin[g];
         }
+    const int64_t tiles = (N + kTileRows - 1) / kTileRows;
     const int b_begin = blockIdx.y * bps;
     const int b_end = min(B, b_begin + bps);
     const int col = lane & 15, q = lane >> 4;
-    const uint8_t *wt = packed + t * (int64_t)B * kTileBytes;
+    const uint8_t *wt[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) // tiles past the weight's last are clamped; stores are masked
+        wt[nt] = packed + min(wg * NT + nt, tiles - 1) * (int64_t)B * kTileBytes;
     const int first = b_begin + wave;
     const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
     const int last = first + (count - 1) * W;
     {
-        const int nt = W * 64;
-        for (int i = tid; i < 512; i += nt)
+        const int nthr = W * 64;
+        for (int i = tid; i < 512; i += nthr)
             s_lvl[i] = c_grid.level[i];
         if (tid < 16)
             s_split[tid] = uint4{c_split.w[tid][0], c_split.w[tid][1], c_split.w[tid][2], c_split.w[tid][3]};
         if constexpr (kLdsAct) {
             const int nx = rows * K / 16;
-            for (int c = tid; c < nx; c += nt) {
+            for (int c = tid; c < nx; c += nthr) {
                 const int r = c * 16 / K;
                 *reinterpret_cast<uint4 *>(smem + L.x + c * 16) =
                     *reinterpret_cast<const uint4 *>(xv + (m0 + r) * ldxv + (c * 16 - r * K));
             }
             const int ns = rows * (K / 32);
-            for (int i = tid; i < ns; i += nt) {
+            for (int i = tid; i < ns; i += nthr) {
                 const int r = i / (K / 32);
                 smem[L.xs + i] = xs[(m0 + r) * ldxs + (i - r * (K / 32))];
             }
@@ -586,13 +593,20 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         soff = (uint32_t)(rowc * ldxs) + so;
     }
 
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[nt][r] = 0.0f;
     if (count > 0) {
-        WTile wr[kDepth];
+        WTile wr[kDepth][NT];
         ADense ar[kLdsAct ? 1 : kDepth];
 #pragma unroll
         for (int j = 0; j < kDepth - 1; ++j) {
-            wr[j] = load_w(wt + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                wr[j][nt] = load_w(wt[nt] + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
                 load_a_dense(ar[j], xbase, xoff, sbase, soff, min(first + j * W, last));
         }
@@ -602,17 +616,18 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                 const int i = i0 + j;
                 const int slot = (j + kDepth - 1) % kDepth;
                 const int bp = min(first + (i + kDepth - 1) * W, last);
-                wr[slot] = load_w(wt + (int64_t)bp * kTileBytes, lane, col);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    wr[slot][nt] = load_w(wt[nt] + (int64_t)bp * kTileBytes, lane, col);
                 if constexpr (!kLdsAct)
                     load_a_dense(ar[slot], xbase, xoff, sbase, soff, bp);
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
-                if constexpr (kLdsAct) {
+                if constexpr (kLdsAct)
                     load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
-                    compute_dense(wr[j], ar[0], lvl, s_split, acc, i < count);
-                } else {
-                    compute_dense(wr[j], ar[j], lvl, s_split, acc, i < count);
-                }
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    compute_dense(wr[j][nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
             }
@@ -624,30 +639,37 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     if constexpr (W > 1) {
         float *red = reinterpret_cast<float *>(smem + L.red);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            red[(wave * 4 + r) * 64 + lane] = acc[r];
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[((wave * NT + nt) * 4 + r) * 64 + lane] = acc[nt][r];
         __syncthreads();
         if (wave != 0)
             return;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float v = 0.0f;
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int w = 0; w < W; ++w)
-                v += red[(w * 4 + r) * 64 + lane];
-            acc[r] = v;
-        }
+            for (int r = 0; r < 4; ++r) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < W; ++w)
+                    v += red[((w * NT + nt) * 4 + r) * 64 + lane];
+                acc[nt][r] = v;
+            }
     }
-    const int64_t n = t * kTileRows + col;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + 4 * q + r;
-        if (m < M && n < N) {
-            float *o = out + m * ldo + n;
-            if (atomic)
-                atomicAdd(o, acc[r]);
-            else
-                *o = acc[r];
+    for (int nt = 0; nt < NT; ++nt) {
+        const int64_t n = (wg * NT + nt) * kTileRows + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + 4 * q + r;
+            if (m < M && n < N) {
+                float *o = out + m * ldo + n;
+                if (atomic)
+                    atomicAdd(o, acc[nt][r]);
+                else
+                    *o = acc[nt][r];
+            }
         }
     }
 }
@@ -668,6 +690,61 @@ constexpr int kTiledPitch = 272;
 __host__ __device__ constexpr int tiled_lds_bytes(int MT)
 {
     return 2 * (16 * MT * kTiledPitch + 16 * MT * 8);
+}
+
+// Decoded dense operands of NT weight tiles for one block (see the dense kernel).
+template <int NT>
+__device__ __forceinline__ void decode_tiles(const WTile (&w)[NT], const uint8_t *lvl, const uint4 *split,
+                                             v8i (&bh)[NT][2], v8i (&bl)[NT][2], float (&d)[NT])
+{
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t s5[5] = {w[nt].ia.x, w[nt].ia.y, w[nt].ia.z, w[nt].ia.w, (uint32_t)w[nt].ib};
+        const uint4 t0 = split[w[nt].sc & 15u], t1 = split[(uint32_t)w[nt].sc >> 4];
+        decode_split<0>(s5, w[nt].sg.x, lvl, t0, bh[nt][0], bl[nt][0], std::make_integer_sequence<int, 8>{});
+        decode_split<1>(s5, w[nt].sg.y, lvl, t1, bh[nt][1], bl[nt][1], std::make_integer_sequence<int, 8>{});
+        to_dense_order(bh[nt][0]);
+        to_dense_order(bl[nt][0]);
+        to_dense_order(bh[nt][1]);
+        to_dense_order(bl[nt][1]);
+        d[nt] = half_bits_to_float((uint16_t)w[nt].dh);
+    }
+}
+
+// MT x NT sub-tiles of one block: A fragments from the staged block (a: values at this
+// lane's row/column offset, sa: scales), one chain of four MFMAs (K halves x hi/lo) per
+// sub-tile, then the block's d in f32. The fence per sub-tile keeps the compiler from
+// hoisting every LDS read of the block into registers.
+template <int MT, int NT>
+__device__ __forceinline__ void mfma_block(const uint8_t *a, const uint8_t *sa, const v8i (&bh)[NT][2],
+                                           const v8i (&bl)[NT][2], const float (&d)[NT], float (&acc)[MT][NT][4])
+{
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t *ar = a + 16 * mt * kTiledPitch;
+        const uint8_t *sr = sa + 16 * mt * 8;
+        v8i av[2];
+        int sc[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 lo = *reinterpret_cast<const uint4 *>(ar + 32 * h);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(ar + 32 * h + 64);
+            av[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            sc[h] = sr[h];
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bh[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bl[nt][0], c, 0, 0, 0, sc[0], 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bh[nt][1], c, 0, 0, 0, sc[1], 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bl[nt][1], c, 0, 0, 0, sc[1], 0, 128);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mt][nt][r] = __builtin_fmaf(c[r], d[nt], acc[mt][nt][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 template <int MT, int NT, int W>
@@ -768,7 +845,11 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     // earlier) and are written to LDS at the top, then refilled with block b+2; the
     // loads are consumed only in the next iteration, so they overlap a whole block of
     // math and cannot be moved down to their stores.
+    const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
+    const uint32_t aoff = (uint32_t)col * kTiledPitch + xo, soff = (uint32_t)col * 8 + so;
     WTile wcur[NT], wnext[NT];
+    v8i bh[NT][2], bl[NT][2];
+    float d[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
         wcur[nt] = load_w(wt[nt], lane, col);
@@ -786,55 +867,9 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
         for (int nt = 0; nt < NT; ++nt)
             wnext[nt] = load_w(wt[nt] + (int64_t)min(b + 1, B - 1) * kTileBytes, lane, col);
         __builtin_amdgcn_sched_barrier(0);
-
-        v8i bh[NT][2], bl[NT][2];
-        float d[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const WTile &w = wcur[nt];
-            const uint32_t s5[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
-            const uint4 t0 = s_split[w.sc & 15u], t1 = s_split[(uint32_t)w.sc >> 4];
-            const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
-            decode_split<0>(s5, w.sg.x, lvl, t0, bh[nt][0], bl[nt][0], std::make_integer_sequence<int, 8>{});
-            decode_split<1>(s5, w.sg.y, lvl, t1, bh[nt][1], bl[nt][1], std::make_integer_sequence<int, 8>{});
-            to_dense_order(bh[nt][0]);
-            to_dense_order(bl[nt][0]);
-            to_dense_order(bh[nt][1]);
-            to_dense_order(bl[nt][1]);
-            d[nt] = half_bits_to_float((uint16_t)w.dh);
-        }
-        const uint8_t *a = smem + (b & 1) * kABytes;
-        const uint8_t *sa = smem + 2 * kABytes + (b & 1) * kSBytes;
-        // A fragments read per sub-tile (the other resident wave of the SIMD covers the LDS
-        // latency); the fence per sub-tile keeps the compiler from hoisting every LDS
-        // read of the block into registers.
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint8_t *ar = a + (16 * mt + col) * kTiledPitch + xo;
-            const uint8_t *sr = sa + (16 * mt + col) * 8 + so;
-            v8i av[2];
-            int sc[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint4 lo = *reinterpret_cast<const uint4 *>(ar + 32 * h);
-                const uint4 hi = *reinterpret_cast<const uint4 *>(ar + 32 * h + 64);
-                av[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-                sc[h] = sr[h];
-            }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-                v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bh[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
-                v4f c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bl[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
-                c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bh[nt][1], c1, 0, 0, 0, sc[1], 0, 128);
-                c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bl[nt][1], c2, 0, 0, 0, sc[1], 0, 128);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[mt][nt][r] = __builtin_fmaf(c1[r] + c2[r], d[nt], acc[mt][nt][r]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);
+        mfma_block<MT, NT>(smem + (b & 1) * kABytes + aoff, smem + 2 * kABytes + (b & 1) * kSBytes + soff, bh, bl, d,
+                           acc);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
             wcur[nt] = wnext[nt];
@@ -908,24 +943,26 @@ int launch_stream_u(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t 
     return MAMBO_OK;
 }
 
-template <int W>
-void launch_dense_w(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                    const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+template <int W, int NT>
+void launch_dense_wn(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                     const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     if (lds_act)
-        hipLaunchKernelGGL((gemm_dense_kernel<W, true>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M, ga, B,
-                           bps, atomic);
+        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, true>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
+                           ga, B, bps, atomic);
     else
-        hipLaunchKernelGGL((gemm_dense_kernel<W, false>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M, ga,
-                           B, bps, atomic);
+        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, false>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
+                           ga, B, bps, atomic);
 }
 
-int launch_dense(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                 const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+template <int NT>
+int launch_dense_n(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
+                   int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
+                   int atomic)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_dense_w<WV>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                  \
+        launch_dense_wn<WV, NT>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);             \
         break;
     switch (waves) {
         MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
@@ -934,6 +971,18 @@ int launch_dense(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t str
     }
 #undef MAMBO_W
     return MAMBO_OK;
+}
+
+int launch_dense(int waves, int nt, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
+                 int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
+                 int atomic)
+{
+    switch (nt) {
+    case 1: return launch_dense_n<1>(waves, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 2: return launch_dense_n<2>(waves, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 4: return launch_dense_n<4>(waves, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    default: return mambo_fail(MAMBO_ERR_VALUE, "dense kernel: tile_n must be 16, 32 or 64 (got %d)", 16 * nt);
+    }
 }
 
 template <int MT, int NT, int W>
@@ -968,14 +1017,20 @@ constexpr int64_t kTargetWaves = 8192;
 // Below this many waves the default config splits K.
 constexpr int64_t kMinWaves = 512;
 // Activations are staged in LDS when the workgroup's rows take at most this much.
-constexpr int kMaxLdsAct = 40 * 1024;
+#ifndef MAMBO_MAX_LDS_ACT_KB
+#define MAMBO_MAX_LDS_ACT_KB 40
+#endif
+constexpr int kMaxLdsAct = MAMBO_MAX_LDS_ACT_KB * 1024;
 // Compute units of an MI355X (the tiled default sizes its grid to at least one
 // workgroup per CU).
 constexpr int64_t kCUs = 256;
 // Token count from which the default configuration uses the tiled kernel.
 constexpr int64_t kTiledMinM = 64;
 // Dynamic LDS per workgroup (the static codebook tables add 2.3 KiB).
-constexpr int kMaxDynLds = 60 * 1024;
+#ifndef MAMBO_MAX_DYN_LDS_KB
+#define MAMBO_MAX_DYN_LDS_KB 60
+#endif
+constexpr int kMaxDynLds = MAMBO_MAX_DYN_LDS_KB * 1024;
 
 bool valid_waves(int w)
 {
@@ -1017,7 +1072,7 @@ extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, m
         *out = c;
         return MAMBO_OK;
     }
-    const int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
+    int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
     // Waves per workgroup: the largest power of two up to 8 (16 for M <= 4 and grids of at
     // most 2K waves; wider sub-tiles spill at 1024 threads) that divides the K blocks evenly, keeps at least two blocks per wave and at
     // most about two residency rounds of waves in the grid (measured on gfx950: deeper
@@ -1029,8 +1084,23 @@ extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, m
         if (units * w <= (w < 16 ? kTargetWaves : kTargetWaves / 4) && (w < 16 || m <= 4) && blocks % w == 0 &&
             blocks / w >= 2)
             waves = w;
+    if (c.kernel == MAMBO_GEMM_DENSE) {
+        // Dense: 4 waves, and as many weight tiles per workgroup (sharing each activation
+        // fragment) as still leave a workgroup per CU; measured on gfx950 at M = 8..16.
+        const int64_t rt = cdiv(n, kTileRows);
+        int nt = 1;
+        for (int t : {2, 4})
+            if (cdiv(rt, t) * cdiv(m, 16) >= kCUs)
+                nt = t;
+        c.tile_n = kTileRows * nt;
+        waves = 1;
+        for (int w : {2, 4})
+            if (blocks % w == 0 && blocks / w >= 2)
+                waves = w;
+        units = cdiv(rt, nt) * cdiv(m, 16);
+    }
     int64_t split = 1;
-    if (units * waves < kMinWaves) {
+    if (units * waves < (c.kernel == MAMBO_GEMM_DENSE ? kMinWaves / 4 : kMinWaves)) {
         const int64_t per_split_waves = units * waves;
         split = std::min<int64_t>(cdiv(kMinWaves, per_split_waves), std::max<int64_t>(1, blocks / (2 * waves)));
     }
@@ -1056,6 +1126,9 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
         return MAMBO_OK;
     }
     MAMBO_REQUIRE(valid_waves(cfg->waves), MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16");
+    if (cfg->kernel == MAMBO_GEMM_DENSE)
+        MAMBO_REQUIRE(cfg->tile_n == 0 || cfg->tile_n == 16 || cfg->tile_n == 32 || cfg->tile_n == 64,
+                      MAMBO_ERR_VALUE, "dense: tile_n must be 16, 32 or 64 weight rows");
     MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                   "split_k must be in [1, K/256]");
     return MAMBO_OK;
@@ -1156,10 +1229,19 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
     const int B = (int)blocks;
     if (c.kernel == MAMBO_GEMM_DENSE) {
-        if (lds_act && dense_lds(c.waves, rows, (int)k, true).total > kMaxDynLds)
+        const int nt = c.tile_n ? c.tile_n / kTileRows : 1;
+        // workgroups per projection (NT tiles each); tile_begin counts workgroups
+        GroupArgs gd = ga;
+        int64_t wgs = 0;
+        for (int g = 0; g < count; ++g) {
+            gd.tile_begin[g] = wgs;
+            wgs += cdiv(cdiv(ga.n[g], kTileRows), nt);
+        }
+        grid.x = (unsigned)wgs;
+        if (lds_act && dense_lds(c.waves, nt, rows, (int)k, true).total > kMaxDynLds)
             lds_act = false;
-        const DenseLds L = dense_lds(c.waves, rows, (int)k, lds_act);
-        rc = launch_dense(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic);
+        const DenseLds L = dense_lds(c.waves, nt, rows, (int)k, lds_act);
+        rc = launch_dense(c.waves, nt, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, gd, B, bps, atomic);
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
         if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > kMaxDynLds)

@@ -252,8 +252,14 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
             if waves > blocks or (kernel == _native.GEMM_STREAM and waves * u > 32):
                 continue
             for split in (1, 2, 4, 8):
-                if split <= blocks // waves:
+                if split > blocks // waves:
+                    continue
+                if kernel == _native.GEMM_STREAM:
                     space.append({"kernel": kernel, "waves": waves, "split_k": split})
+                else:  # weight tiles per workgroup sharing one activation fragment
+                    for rows in (16, 32, 64):
+                        if waves * rows <= 256:
+                            space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows})
     if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup
         for tile_m in (64, 128):
             for waves in (4, 8):
