@@ -151,7 +151,9 @@ def run_gemm(args):
         graph.replay()
         torch.cuda.synchronize()
         for o, r in zip(outputs, ref):
-            if not torch.allclose(o, r, rtol=1e-5, atol=1e-5):
+            # K-split launches add partial sums with f32 atomics, whose order varies from
+            # run to run: allow last-bit differences relative to the output's scale
+            if not torch.allclose(o, r, rtol=1e-4, atol=1e-5 * float(r.abs().max())):
                 diff = (o - r).abs().max().item()
                 raise RuntimeError(f"graph replay differs from eager launch (output {tuple(o.shape)}: max diff "
                                    f"{diff}, nan {int(torch.isnan(o).sum())}, ref nan {int(torch.isnan(r).sum())})")

@@ -750,7 +750,7 @@ __device__ __forceinline__ void mfma_block(const uint8_t *a, const uint8_t *sa, 
 template <int MT, int NT, int W>
 __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
-                                                            GroupArgs ga, int B)
+                                                            GroupArgs ga, int B, int bps, int atomic)
 {
     constexpr int kRows = 16 * MT;
     constexpr int kABytes = kRows * kTiledPitch;
@@ -847,25 +847,28 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     // math and cannot be moved down to their stores.
     const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
     const uint32_t aoff = (uint32_t)col * kTiledPitch + xo, soff = (uint32_t)col * 8 + so;
+    // K range of this workgroup: blocks [b0, b1) (grid z splits K; partial sums are
+    // added into an output zeroed beforehand)
+    const int b0 = blockIdx.z * bps, b1 = min(B, b0 + bps);
     WTile wcur[NT], wnext[NT];
     v8i bh[NT][2], bl[NT][2];
     float d[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-        wcur[nt] = load_w(wt[nt], lane, col);
-    MAMBO_LOAD_STAGE(0);
-    MAMBO_STORE_STAGE(0);
-    MAMBO_LOAD_STAGE(min(1, B - 1));
+        wcur[nt] = load_w(wt[nt] + (int64_t)b0 * kTileBytes, lane, col);
+    MAMBO_LOAD_STAGE(b0);
+    MAMBO_STORE_STAGE(b0 & 1);
+    MAMBO_LOAD_STAGE(min(b0 + 1, b1 - 1));
     __syncthreads();
 
-    for (int b = 0; b < B; ++b) {
+    for (int b = b0; b < b1; ++b) {
         // buffer (b+1)&1 was last read in block b-1, before the previous barrier; after
         // the last block this fills the idle buffer
         MAMBO_STORE_STAGE((b + 1) & 1);
-        MAMBO_LOAD_STAGE(min(b + 2, B - 1));
+        MAMBO_LOAD_STAGE(min(b + 2, b1 - 1));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-            wnext[nt] = load_w(wt[nt] + (int64_t)min(b + 1, B - 1) * kTileBytes, lane, col);
+            wnext[nt] = load_w(wt[nt] + (int64_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);
         __builtin_amdgcn_sched_barrier(0);
         decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);
         mfma_block<MT, NT>(smem + (b & 1) * kABytes + aoff, smem + 2 * kABytes + (b & 1) * kSBytes + soff, bh, bl, d,
@@ -888,8 +891,12 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t m = m0 + 16 * mt + 4 * q + r;
-                if (m < M)
-                    out[m * ldo + n] = acc[mt][nt][r];
+                if (m < M) {
+                    if (atomic)
+                        atomicAdd(out + m * ldo + n, acc[mt][nt][r]);
+                    else
+                        out[m * ldo + n] = acc[mt][nt][r];
+                }
             }
     }
 #undef MAMBO_LOAD_STAGE
@@ -987,19 +994,19 @@ int launch_dense(int waves, int nt, bool lds_act, dim3 grid, size_t lds, hipStre
 
 template <int MT, int NT, int W>
 void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
-                    int64_t M, const GroupArgs &ga, int B)
+                    int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv, ldxv, xs,
-                       ldxs, M, ga, B);
+                       ldxs, M, ga, B, bps, atomic);
 }
 
 // Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves).
 int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                 const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B)
+                 const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
 #define MAMBO_T(A, C, D)                                                                                           \
     if (mt == A && nt == C && waves == D) {                                                                        \
-        launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B);                                       \
+        launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                          \
         return MAMBO_OK;                                                                                           \
     }
     MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
@@ -1042,43 +1049,55 @@ bool valid_waves(int w)
 
 } // namespace
 
-extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out)
+namespace {
+
+// Default configuration of `kernel` (MAMBO_GEMM_AUTO: the family chosen by M) for the shape.
+mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t blocks)
 {
-    MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
-    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
     mambo_gemm_config c = {};
     // Block-diagonal activations cost nothing extra while one MFMA covers every token
     // (M <= 4); beyond that the dense kernel does 4 MFMAs per block for 16 tokens where
-    // the block-diagonal one needs 2 per 4 tokens and an activation sub-tile each.
-    c.kernel = m <= 4 ? MAMBO_GEMM_STREAM : m < kTiledMinM ? MAMBO_GEMM_DENSE : MAMBO_GEMM_TILED;
+    // the block-diagonal one needs 2 per 4 tokens and an activation sub-tile each; the
+    // tiled kernel from 64 tokens.
+    c.kernel = kernel != MAMBO_GEMM_AUTO ? kernel
+               : m <= 4                  ? MAMBO_GEMM_STREAM
+               : m < kTiledMinM          ? MAMBO_GEMM_DENSE
+                                         : MAMBO_GEMM_TILED;
     if (c.kernel == MAMBO_GEMM_TILED) {
         // The largest tile that still gives every CU a workgroup (measured on gfx950:
         // 128 tokens x 256 weight rows x 8 waves is fastest when the grid fills the chip;
-        // 64 x 128 x 8, then 64 x 64 x 4, for small N x M).
+        // then 64 x 128 x 8 and 64 x 64 x 4); when even the smallest leaves CUs idle, K
+        // is split (at least 8 blocks per split) until the grid covers the chip twice.
         const int64_t rt = cdiv(n, kTileRows);
         c.split_k = 1;
         c.waves = 8;
-        if (cdiv(rt, 16) * cdiv(m, 128) >= kCUs) {
+        int64_t wgs;
+        if ((wgs = cdiv(rt, 16) * cdiv(m, 128)) >= kCUs) {
             c.tile_m = 128;
             c.tile_n = 256;
-        } else if (cdiv(rt, 8) * cdiv(m, 64) >= kCUs) {
+        } else if ((wgs = cdiv(rt, 8) * cdiv(m, 64)) >= kCUs) {
             c.tile_m = 64;
             c.tile_n = 128;
         } else {
             c.tile_m = 64;
-            c.tile_n = 64;
-            c.waves = 4;
+            c.tile_n = 128;
+            wgs = cdiv(rt, 8) * cdiv(m, 64);
+            c.split_k = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv(2 * kCUs, wgs), blocks / 8));
         }
-        *out = c;
-        return MAMBO_OK;
+        // Few weight rows (k/v projections) leave even the split grid small: up to 255
+        // tokens the dense kernel's 16-token chunks are faster there (measured).
+        if (kernel == MAMBO_GEMM_AUTO && m < 256 && wgs * c.split_k < kCUs / 2)
+            return family_default(MAMBO_GEMM_DENSE, m, n, blocks);
+        return c;
     }
     int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
     // Waves per workgroup: the largest power of two up to 8 (16 for M <= 4 and grids of at
-    // most 2K waves; wider sub-tiles spill at 1024 threads) that divides the K blocks evenly, keeps at least two blocks per wave and at
-    // most about two residency rounds of waves in the grid (measured on gfx950: deeper
-    // oversubscription and uneven splits both lose). K is split only when even that
-    // leaves the chip mostly idle: a split costs a zero fill and atomics, which lose to
-    // wider workgroups down to ~1K waves.
+    // most 2K waves; wider sub-tiles spill at 1024 threads) that divides the K blocks
+    // evenly, keeps at least two blocks per wave and at most about two residency rounds
+    // of waves in the grid (measured on gfx950: deeper oversubscription and uneven
+    // splits both lose). K is split only when even that leaves the chip mostly idle: a
+    // split costs a zero fill and atomics, which lose to wider workgroups down to ~1K
+    // waves.
     int waves = 1;
     for (int w : {2, 4, 8, 16})
         if (units * w <= (w < 16 ? kTargetWaves : kTargetWaves / 4) && (w < 16 || m <= 4) && blocks % w == 0 &&
@@ -1106,7 +1125,16 @@ extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, m
     }
     c.waves = waves;
     c.split_k = (int32_t)std::max<int64_t>(split, 1);
-    *out = c;
+    return c;
+}
+
+} // namespace
+
+extern "C" int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out)
+{
+    MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
+    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
+    *out = family_default(MAMBO_GEMM_AUTO, m, n, blocks);
     return MAMBO_OK;
 }
 
@@ -1122,7 +1150,8 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
         MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE, "tiled: waves must be 4 or 8");
         MAMBO_REQUIRE(cfg->tile_n == 16 * cfg->waves || cfg->tile_n == 32 * cfg->waves, MAMBO_ERR_VALUE,
                       "tiled: tile_n must be 16 or 32 weight rows per wave");
-        MAMBO_REQUIRE(cfg->split_k == 1, MAMBO_ERR_VALUE, "tiled: split_k must be 1");
+        MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
+                      "split_k must be in [1, K/256]");
         return MAMBO_OK;
     }
     MAMBO_REQUIRE(valid_waves(cfg->waves), MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16");
@@ -1168,14 +1197,13 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         tiles += cdiv(p.n, kTileRows);
         n_total += p.n;
     }
-    // Library default for the shape, overlaid with the non-zero fields of cfg.
-    mambo_gemm_config c;
-    int rc = mambo_gemm_default_config(m, n_total, blocks, &c);
-    if (rc)
-        return rc;
+    // Library default of the requested kernel family (or of the family chosen by M),
+    // overlaid with the non-zero fields of cfg.
+    MAMBO_REQUIRE(cfg == nullptr || (cfg->kernel >= MAMBO_GEMM_AUTO && cfg->kernel <= MAMBO_GEMM_DENSE),
+                  MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg ? cfg->kernel : 0);
+    mambo_gemm_config c = family_default(cfg ? cfg->kernel : MAMBO_GEMM_AUTO, m, n_total, blocks);
+    int rc = MAMBO_OK;
     if (cfg != nullptr) {
-        if (cfg->kernel != MAMBO_GEMM_AUTO)
-            c.kernel = cfg->kernel;
         if (cfg->waves)
             c.waves = cfg->waves;
         if (cfg->split_k)
@@ -1187,6 +1215,19 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         rc = mambo_gemm_check_config(m, n_total, blocks, &c);
         if (rc)
             return rc;
+    }
+    const int bps = (int)cdiv(blocks, c.split_k);
+    const int splits = (int)cdiv(blocks, bps);
+    const int atomic = splits > 1;
+    if (atomic) {
+        MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
+        for (int g = 0; g < count; ++g) {
+            dim3 zg((unsigned)std::min<int64_t>(cdiv(ga.n[g], 256), 1024), (unsigned)m);
+            hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, ga.out[g], m, ga.n[g], ga.ldo[g]);
+            rc = mambo_check_launch("zero_rows");
+            if (rc)
+                return rc;
+        }
     }
     if (c.kernel == MAMBO_GEMM_TILED) {
         const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);
@@ -1201,27 +1242,14 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         }
         const int64_t mtiles = cdiv(m, c.tile_m);
         MAMBO_REQUIRE(wgs <= 0x7FFFFFFF && mtiles <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
-        rc = launch_tiled(mt, nt, c.waves, dim3((unsigned)wgs, (unsigned)mtiles), s, xv, ldxv, xs, ldxs, m, gt,
-                          (int)blocks);
+        rc = launch_tiled(mt, nt, c.waves, dim3((unsigned)wgs, (unsigned)mtiles, (unsigned)splits), s, xv, ldxv, xs,
+                          ldxs, m, gt, (int)blocks, bps, atomic);
         if (rc)
             return rc;
         return mambo_check_launch("iq3s_fp8_matmul (tiled)");
     }
     const int64_t mchunks = cdiv(m, 16);
     MAMBO_REQUIRE(tiles <= 0x7FFFFFFF && mchunks <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
-    const int bps = (int)cdiv(blocks, c.split_k);
-    const int splits = (int)cdiv(blocks, bps);
-    const int atomic = splits > 1;
-    if (atomic) {
-        MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
-        for (int g = 0; g < count; ++g) {
-            dim3 zg((unsigned)std::min<int64_t>(cdiv(ga.n[g], 256), 1024), (unsigned)m);
-            hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, ga.out[g], m, ga.n[g], ga.ldo[g]);
-            rc = mambo_check_launch("zero_rows");
-            if (rc)
-                return rc;
-        }
-    }
     const int rows = (int)std::min<int64_t>(16, m); // rows of the largest M chunk
     // Stage the activations in LDS when they are small enough; otherwise read them from
     // global memory (L2) in the weight ring.

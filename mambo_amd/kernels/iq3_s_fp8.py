@@ -260,12 +260,14 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
                     for rows in (16, 32, 64):
                         if waves * rows <= 256:
                             space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows})
-    if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup
+    if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup x K split
         for tile_m in (64, 128):
             for waves in (4, 8):
                 for rows_per_wave in (16, 32):
-                    space.append({"kernel": _native.GEMM_TILED, "waves": waves, "split_k": 1, "tile_m": tile_m,
-                                  "tile_n": rows_per_wave * waves})
+                    for split in (1, 2, 4):
+                        if split <= blocks:
+                            space.append({"kernel": _native.GEMM_TILED, "waves": waves, "split_k": split,
+                                          "tile_m": tile_m, "tile_n": rows_per_wave * waves})
     return space
 
 

@@ -77,18 +77,28 @@ def test_gemm_config_defaults_and_validation():
     ok = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 128,
                                        "tile_n": 128})
     assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(ok)) == 0
-    for bad_fields in ({"tile_m": 96}, {"waves": 2, "tile_n": 32}, {"tile_n": 96}, {"split_k": 2}):
+    for bad_fields in ({"tile_m": 96}, {"waves": 2, "tile_n": 32}, {"tile_n": 96}, {"split_k": 5}):
         bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 128,
                                             "tile_n": 128, **bad_fields})
         assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE, bad_fields
-    # block-diagonal activations up to M=4, dense up to 63, tiled from 64
-    for m, kernel in ((1, _native.GEMM_STREAM), (4, _native.GEMM_STREAM), (5, _native.GEMM_DENSE),
-                      (16, _native.GEMM_DENSE), (63, _native.GEMM_DENSE), (64, _native.GEMM_TILED),
-                      (2048, _native.GEMM_TILED)):
+    split = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 4, "tile_m": 128,
+                                          "tile_n": 128})
+    assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(split)) == 0
+    # moderate M on a long K: the tiled default splits K to fill the chip
+    c = _native.GemmConfig()
+    assert lib.mambo_gemm_default_config(64, 8192, 112, ctypes.byref(c)) == 0
+    assert c.kernel == _native.GEMM_TILED and c.split_k > 1, c.as_dict()
+    # block-diagonal activations up to M=4, dense up to 63, tiled from 64 - except for
+    # few weight rows below 256 tokens, where the tiled grid stays small
+    for m, n, kernel in ((1, 8192, _native.GEMM_STREAM), (4, 8192, _native.GEMM_STREAM),
+                         (5, 8192, _native.GEMM_DENSE), (16, 8192, _native.GEMM_DENSE),
+                         (63, 8192, _native.GEMM_DENSE), (64, 8192, _native.GEMM_TILED),
+                         (2048, 8192, _native.GEMM_TILED), (128, 1024, _native.GEMM_DENSE),
+                         (256, 1024, _native.GEMM_TILED)):
         c = _native.GemmConfig()
-        assert lib.mambo_gemm_default_config(m, 4096, 16, ctypes.byref(c)) == 0
-        assert c.kernel == kernel, (m, c.as_dict())
-        assert lib.mambo_gemm_check_config(m, 4096, 16, ctypes.byref(c)) == 0
+        assert lib.mambo_gemm_default_config(m, n, 32, ctypes.byref(c)) == 0
+        assert c.kernel == kernel, (m, n, c.as_dict())
+        assert lib.mambo_gemm_check_config(m, n, 32, ctypes.byref(c)) == 0
 
 
 def test_codebook_exports_match_python_tables():
