@@ -165,7 +165,7 @@ def load_gguf_weight(model: Path, weight_name: str, expected_type: str) -> torch
         raise ValueError(f"{weight_name} has an inconsistent GGUF block layout")
     raw = np.memmap(model, mode="r", dtype=np.uint8, offset=tensor["offset"]["absolute"],
                     shape=(n_rows, k // block_values, block_bytes))
-    return torch.from_numpy(np.ascontiguousarray(raw)).cuda()
+    return torch.from_numpy(np.array(raw)).cuda()  # a writable host copy of the mapped bytes
 
 
 def synthetic_weight(n: int, k: int, seed: int = 0) -> torch.Tensor:

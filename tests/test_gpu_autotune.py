@@ -1,0 +1,84 @@
+"""The autotuner end to end on the GPU (kernel_benchmark.py:27-141 semantics): every
+candidate of the search space runs, the winner's output matches the oracle, the tuned
+table is written and then used by launch_iq3_s_fp8_matmul; and a weight read from a GGUF
+file goes through the same path."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2
+from oracle import oracle
+from test_tuning import write_gguf
+
+pytestmark = pytest.mark.gpu
+
+
+def step(msg: str) -> None:
+    print(f"[gpu] {msg}", flush=True)
+
+
+def test_autotune_search_winner_and_table(gpu, tmp_path, monkeypatch):
+    from mambo_amd.kernels import iq3_s_fp8
+    from mambo_amd.utils.kernel_benchmark import mini_benchmark, synthetic_weight, write_tuned_table
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n, k = 256, 2048
+    step(f"synthetic weight {n}x{k}, tune M=4 and M=64")
+    raw = synthetic_weight(n, k, seed=11)
+    cases = iq3_s_fp8.make_benchmark_cases(raw, tokens=(4, 64))
+    results = mini_benchmark(cases, quiet=True)
+    assert [r.key for r in results] == [iq3_s_fp8.tuned_key(n, k, 4), iq3_s_fp8.tuned_key(n, k, 64)]
+    for case, r in zip(cases, results):
+        assert r.best in list(case.search_space)
+        assert not r.failures, r.failures[:3]
+        assert len(r.successes) == len(case.search_space)
+        assert r.event_us > 0 and r.mean_us > 0 and r.batched_us > 0
+    # the winners reproduce the oracle
+    fields = prepare_iq3_s_fields(raw)
+    raw_np = raw.cpu().numpy()
+    for m, r in zip((4, 64), results):
+        x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+        xv, xs = oracle.quantize_mxfp8(x)
+        step(f"winner M={m}: {r.best}")
+        out = iq3_s_fp8.launch_iq3_s_fp8_matmul(torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu), fields,
+                                                config=r.best)
+        torch.cuda.synchronize()
+        assert rel_l2(out.cpu().numpy(), oracle.iq3s_fp8_matmul(xv, xs, raw_np)) <= 1e-3
+    # the table is written and then consulted by the launcher's config selection
+    path = tmp_path / "tuned.json"
+    write_tuned_table(results, path, "gfx950")
+    monkeypatch.setattr(iq3_s_fp8, "TUNED_PATH", path)
+    iq3_s_fp8._tuned_table.cache_clear()
+    try:
+        assert iq3_s_fp8.select_config(4, n, k, arch="gfx950") == results[0].best
+        assert iq3_s_fp8.select_config(64, n, k, arch="gfx950") == results[1].best
+    finally:
+        iq3_s_fp8._tuned_table.cache_clear()
+
+
+def test_gguf_weight_through_the_projection(gpu, tmp_path):
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    from mambo_amd.utils.kernel_benchmark import load_gguf_weight
+    n, k = 40, 1024
+    raw = oracle.gen_iq3s(21, n, k // 256)
+    path = tmp_path / "m.gguf"
+    write_gguf(path, [("output_norm.weight", [16], 0, np.ones(16, np.float32).tobytes()),
+                      ("blk.0.attn_q.weight", [k, n], 21, raw.tobytes())])
+    step("load GGUF tensor, prepare, quantize, matmul")
+    w = load_gguf_weight(path, "blk.0.attn_q.weight", "iq3_s")
+    assert tuple(w.shape) == (n, k // 256, 110) and w.is_cuda
+    np.testing.assert_array_equal(w.cpu().numpy(), raw)
+    x = np.random.default_rng(5).standard_normal((3, k)).astype(np.float32)
+    xq, xs = launch_quantize_fp8(torch.from_numpy(x).to(gpu))
+    out = launch_iq3_s_fp8_matmul(xq, xs, prepare_iq3_s_fields(w))
+    torch.cuda.synchronize()
+    expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw)
+    assert rel_l2(out.cpu().numpy(), expected) <= 1e-3
+    with pytest.raises(ValueError, match="no tensor named"):
+        load_gguf_weight(path, "missing", "iq3_s")
+    with pytest.raises(ValueError, match="2D iq3_s"):
+        load_gguf_weight(path, "output_norm.weight", "iq3_s")

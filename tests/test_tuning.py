@@ -1,0 +1,107 @@
+"""Autotuner plumbing and the GGUF tensor directory on the CPU (no kernel launches).
+
+The GGUF files are written by the test itself: a v3 header, metadata of several types
+(the reader must skip them), an IQ3_S tensor in ggml ne order [K, N] and an F32 tensor,
+with the data section aligned to general.alignment (kernel_benchmark.py:103-122,
+gguf_manifest.py:435-545 describe the format the reference reads)."""
+
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+
+def _gguf_string(s: str) -> bytes:
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def write_gguf(path, tensors, alignment=32, extra_meta=True, misalign=False):
+    """tensors: list of (name, ne dims, ggml type id, payload bytes)."""
+    meta = [("general.alignment", 4, struct.pack("<I", alignment))]
+    if extra_meta:
+        meta += [("general.name", 8, _gguf_string("synthetic")),
+                 ("tokenizer.ggml.scores", 9, struct.pack("<IQ", 6, 3) + struct.pack("<3f", 0.5, 1.5, 2.5)),
+                 ("tokenizer.ggml.tokens", 9, struct.pack("<IQ", 8, 2) + _gguf_string("a") + _gguf_string("bc")),
+                 ("llama.block_count", 5, struct.pack("<i", 2))]
+    out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta)))
+    for key, type_id, value in meta:
+        out += _gguf_string(key) + struct.pack("<I", type_id) + value
+    offsets, rel = [], 0
+    for _, _, _, payload in tensors:
+        offsets.append(rel + (8 if misalign else 0))
+        rel += (len(payload) + alignment - 1) // alignment * alignment + alignment
+    for (name, dims, type_id, _), off in zip(tensors, offsets):
+        out += _gguf_string(name) + struct.pack("<I", len(dims)) + struct.pack("<" + "Q" * len(dims), *dims)
+        out += struct.pack("<IQ", type_id, off)
+    data_offset = (len(out) + alignment - 1) // alignment * alignment
+    out += bytes(data_offset - len(out))
+    blob = bytearray(rel + 64)
+    for (_, _, _, payload), off in zip(tensors, offsets):
+        blob[off:off + len(payload)] = payload
+    path.write_bytes(bytes(out) + bytes(blob))
+    return data_offset, offsets
+
+
+def test_gguf_directory_of_iq3_s_tensor(tmp_path):
+    from mambo_amd.utils.gguf import inspect_gguf
+    n, k = 3, 512
+    raw = oracle.gen_iq3s(7, n, k // 256)
+    f32 = np.arange(10, dtype=np.float32)
+    path = tmp_path / "m.gguf"
+    data_offset, offsets = write_gguf(path, [("blk.0.ffn_up.weight", [k, n], 21, raw.tobytes()),
+                                             ("output_norm.weight", [10], 0, f32.tobytes())])
+    manifest = inspect_gguf(path)
+    assert manifest["gguf"]["version"] == 3 and manifest["gguf"]["alignment"] == 32
+    assert manifest["gguf"]["data_offset"] == data_offset
+    t0, t1 = manifest["tensors"]
+    assert t0["name"] == "blk.0.ffn_up.weight" and t0["shape"] == [k, n]
+    assert t0["type"]["name"] == "iq3_s" and (t0["type"]["block_elements"], t0["type"]["block_bytes"]) == (256, 110)
+    assert t0["row_bytes"] == 2 * 110 and t0["n_bytes"] == n * 2 * 110
+    assert t0["offset"]["absolute"] == data_offset + offsets[0]
+    blob = path.read_bytes()
+    got = np.frombuffer(blob, dtype=np.uint8, count=t0["n_bytes"], offset=t0["offset"]["absolute"])
+    np.testing.assert_array_equal(got.reshape(n, 2, 110), raw)
+    assert t1["type"]["name"] == "f32" and t1["n_bytes"] == 40
+
+
+def test_gguf_rejects_bad_files(tmp_path):
+    from mambo_amd.utils.gguf import GGUFError, inspect_gguf
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"GGML" + bytes(60))
+    with pytest.raises(GGUFError, match="not a GGUF"):
+        inspect_gguf(bad)
+    mis = tmp_path / "mis.gguf"
+    write_gguf(mis, [("w", [256, 1], 21, bytes(110))], misalign=True)
+    with pytest.raises(GGUFError, match="not aligned"):
+        inspect_gguf(mis)
+    trunc = tmp_path / "trunc.gguf"
+    write_gguf(trunc, [("w", [256, 4], 21, bytes(440))])
+    trunc.write_bytes(trunc.read_bytes()[:-500])
+    with pytest.raises(GGUFError, match="past the end"):
+        inspect_gguf(trunc)
+
+
+def test_tuned_table_round_trip_and_lookup(tmp_path, monkeypatch):
+    from mambo_amd.kernels import iq3_s_fp8
+    from mambo_amd.utils.kernel_benchmark import TuneResult, write_tuned_table
+    path = tmp_path / "tuned.json"
+    best = {"kernel": 3, "waves": 2, "split_k": 1, "tile_n": 32}
+    r = TuneResult("M=16", iq3_s_fp8.tuned_key(4096, 4096, 16), best, 1.0, 1.0, 1.0, 1.0)
+    write_tuned_table([r], path, "gfx950")
+    other = TuneResult("M=4", iq3_s_fp8.tuned_key(4096, 4096, 4), {"kernel": 1, "waves": 4, "split_k": 1},
+                       1.0, 1.0, 1.0, 1.0)
+    write_tuned_table([other], path, "gfx950")  # merges into the existing table
+    monkeypatch.setattr(iq3_s_fp8, "TUNED_PATH", path)
+    iq3_s_fp8._tuned_table.cache_clear()
+    try:
+        assert iq3_s_fp8.select_config(16, 4096, 4096, arch="gfx950") == best
+        assert iq3_s_fp8.select_config(13, 4096, 4096, arch="gfx950") == best  # same M bucket
+        assert iq3_s_fp8.select_config(3, 4096, 4096, arch="gfx950")["waves"] == 4
+        assert iq3_s_fp8.select_config(17, 4096, 4096, arch="gfx950") == iq3_s_fp8.BEST_CONFIGS["gfx950"]["medium"]
+    finally:
+        iq3_s_fp8._tuned_table.cache_clear()
