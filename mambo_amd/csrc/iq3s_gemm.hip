@@ -1091,18 +1091,20 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         return c;
     }
     int64_t units = cdiv(n, kTileRows) * cdiv(m, 16); // workgroups before any K split
-    // Waves per workgroup: the largest power of two up to 8 (16 for M <= 4 and grids of at
-    // most 2K waves; wider sub-tiles spill at 1024 threads) that divides the K blocks
-    // evenly, keeps at least two blocks per wave and at most about two residency rounds
-    // of waves in the grid (measured on gfx950: deeper oversubscription and uneven
-    // splits both lose). K is split only when even that leaves the chip mostly idle: a
-    // split costs a zero fill and atomics, which lose to wider workgroups down to ~1K
-    // waves.
+    // Waves per workgroup (block-diagonal kernel, measured on gfx950 at M = 1): 8 when that
+    // keeps at least 4 K blocks per wave or the grid is small; 4 when 8 would leave large
+    // grids with short waves; 16 for tiny grids (at most 2K waves) at M <= 4 (wider
+    // sub-tiles spill at 1024 threads). The count must divide the K blocks evenly.
+    // K is split only when even that leaves the chip mostly idle: a split costs a zero
+    // fill and atomics, which lose to wider workgroups down to ~1K waves.
     int waves = 1;
-    for (int w : {2, 4, 8, 16})
-        if (units * w <= (w < 16 ? kTargetWaves : kTargetWaves / 4) && (w < 16 || m <= 4) && blocks % w == 0 &&
-            blocks / w >= 2)
+    for (int w : {2, 4})
+        if (blocks % w == 0 && blocks / w >= 2)
             waves = w;
+    if (blocks % 8 == 0 && blocks / 8 >= 2 && (blocks / 8 >= 4 || units * 4 < 4096))
+        waves = 8;
+    if (m <= 4 && units * 16 <= kTargetWaves / 4 && blocks % 16 == 0 && blocks / 16 >= 2)
+        waves = 16;
     if (c.kernel == MAMBO_GEMM_DENSE) {
         // Dense: 4 waves, and as many weight tiles per workgroup (sharing each activation
         // fragment) as still leave a workgroup per CU; measured on gfx950 at M = 8..16.

@@ -57,10 +57,11 @@ def test_gemm_config_defaults_and_validation():
     cfg = _native.GemmConfig()
     assert lib.mambo_gemm_default_config(1, 4096, 16, ctypes.byref(cfg)) == 0
     assert cfg.kernel == _native.GEMM_STREAM and cfg.waves in (1, 2, 4, 6, 8, 12, 16) and 1 <= cfg.split_k <= 16
-    # about two residency rounds of waves, power-of-two waves dividing the blocks evenly,
-    # 16 waves only for small grids, K split only below 512 waves
-    for n, blocks, waves, split in ((28672, 32, 4, 1), (8192, 32, 8, 1), (8192, 112, 8, 1), (10240, 32, 8, 1),
-                                    (57344, 32, 2, 1), (1024, 32, 16, 1), (1024, 16, 8, 1), (64, 64, 16, 2)):
+    # 8 waves with at least 4 blocks each (or small grids), 4 for large grids of short K,
+    # 16 for tiny grids, K split only below 512 waves
+    for n, blocks, waves, split in ((28672, 32, 8, 1), (8192, 32, 8, 1), (8192, 112, 8, 1), (10240, 32, 8, 1),
+                                    (57344, 32, 8, 1), (28672, 16, 4, 1), (4096, 16, 8, 1), (1024, 32, 16, 1),
+                                    (1024, 16, 8, 1), (64, 64, 16, 2)):
         big = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(1, n, blocks, ctypes.byref(big)) == 0
         assert (big.waves, big.split_k) == (waves, split), (n, blocks, big.as_dict())
