@@ -48,10 +48,7 @@ constexpr int kDepth = MAMBO_STREAM_DEPTH;
 #ifndef MAMBO_SCHED_FENCE
 #define MAMBO_SCHED_FENCE 1
 #endif
-// Accumulation chains of the dense kernel's four MFMAs per block (hi and lo terms).
-#ifndef MAMBO_DENSE_CHAINS
-#define MAMBO_DENSE_CHAINS 2
-#endif
+
 
 
 struct WTile {
@@ -315,11 +312,15 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
                 // keep the prefetch issued before the decode of block i (scheduler fence)
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
-                if constexpr (kLdsAct) {
-                    load_a<U>(ar[0], al, min(first + i * W, last));
-                    compute_block<U>(wr[j], ar[0], lut, acc, i < count);
-                } else {
-                    compute_block<U>(wr[j], ar[j], lut, acc, i < count);
+                // blocks past the wave's range (the ring's tail) skip the math; the branch
+                // is wave-uniform and the loads above stay unconditional
+                if (i < count) {
+                    if constexpr (kLdsAct) {
+                        load_a<U>(ar[0], al, min(first + i * W, last));
+                        compute_block<U>(wr[j], ar[0], lut, acc, i < count);
+                    } else {
+                        compute_block<U>(wr[j], ar[j], lut, acc, i < count);
+                    }
                 }
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
@@ -476,18 +477,11 @@ __device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, 
     to_dense_order(l1);
     // B scale 2^1: the split terms are stored halved
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-#if MAMBO_DENSE_CHAINS == 1
-    v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, c, 0, 0, 0, (int)at.s[0], 0, 128);
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c, 0, 0, 0, (int)at.s[1], 0, 128);
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c, 0, 0, 0, (int)at.s[1], 0, 128);
-#else
     v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
     v4f c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
     c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c1, 0, 0, 0, (int)at.s[1], 0, 128);
     c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c2, 0, 0, 0, (int)at.s[1], 0, 128);
     const v4f c = c1 + c2;
-#endif
     const float f = valid ? half_bits_to_float((uint16_t)w.dh) : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
