@@ -165,9 +165,10 @@ __device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at
 }
 
 // Dynamic LDS of the stream kernel (the codebook sits in static LDS, so its address is a
-// compile-time constant folded into the reads): cross-wave partial sums of one 4-row
-// sub-tile [W][4][64] f32, a zero chunk + unit scales for lanes off the block diagonal,
-// and - when kLdsAct - the workgroup's activation rows [rows][K] and scales [rows][K/32].
+// compile-time constant folded into the reads): cross-wave partial sums of a tile,
+// [2][W][U][4][16] f32 (double-buffered, so one barrier per tile suffices), a zero chunk
+// + unit scales for lanes off the block diagonal, and - when kLdsAct - the workgroup's
+// activation rows [rows][K] and scales [rows][K/32].
 struct StreamLds {
     int red, zero, x, xs, total;
 };
@@ -176,17 +177,15 @@ __host__ __device__ inline StreamLds stream_lds(int U, int W, int rows, int K, b
 {
     StreamLds l;
     l.red = 0;
-    l.zero = l.red + (W > 1 ? W * 4 * 64 * 4 : 0);
-    (void)U;
+    l.zero = l.red + (W > 1 ? 2 * W * U * 4 * 16 * 4 : 0);
     l.x = l.zero + 80;
     l.xs = l.x + (lds_act ? rows * K : 0);
     l.total = l.xs + (lds_act ? rows * (K / 32) : 0);
     return l;
 }
 
-// Projections of one launch: they share the activations and K; the grid's x dimension
-// runs over the 16-row tiles of all of them, projection g owning tiles
-// [tile_begin[g], tile_begin[g+1]).
+// Projections of one launch: they share the activations and K; their 16-row tiles are
+// numbered consecutively, projection g owning tiles [tile_begin[g], tile_begin[g+1]).
 constexpr int kMaxGroup = MAMBO_MAX_GROUP;
 struct GroupArgs {
     const uint8_t *packed[kMaxGroup];
@@ -197,10 +196,126 @@ struct GroupArgs {
     int count;
 };
 
+// Tile t of a launch: its first super-block, and its projection's output, N, row stride
+// and tile index within the projection. Only constant indices into the arguments, so
+// everything stays in scalar registers.
+struct TileRef {
+    const uint8_t *w;
+    float *out;
+    int64_t n, ldo, lt;
+};
+
+__device__ __forceinline__ TileRef tile_ref(const GroupArgs &ga, int64_t t, int B)
+{
+    TileRef r = {ga.packed[0], ga.out[0], ga.n[0], ga.ldo[0], t};
+#pragma unroll
+    for (int g = 1; g < kMaxGroup; ++g)
+        if (g < ga.count && t >= ga.tile_begin[g]) {
+            r.w = ga.packed[g];
+            r.out = ga.out[g];
+            r.n = ga.n[g];
+            r.ldo = ga.ldo[g];
+            r.lt = t - ga.tile_begin[g];
+        }
+    r.w += r.lt * (int64_t)B * kTileBytes;
+    return r;
+}
+
+// Position of a wave in its workgroup's run of (tile, step) pairs: step i of a tile is
+// super-block first + i*W; `w` is the tile's first super-block.
+struct StreamCursor {
+    int s, i;
+    int64_t t;
+    const uint8_t *w;
+};
+
+// Move to the next pair unless at the last one (the ring's tail keeps re-reading it).
+__device__ __forceinline__ void advance(StreamCursor &c, int total, int steps, const GroupArgs &ga, int B)
+{
+    if (c.s + 1 < total) {
+        ++c.s;
+        if (++c.i == steps) {
+            c.i = 0;
+            ++c.t;
+            c.w = tile_ref(ga, c.t, B).w;
+        }
+    }
+}
+
+// End of a tile: sum the wave's four K chunks (lane groups), then the waves' sums through
+// LDS, store (or add, when K is split over workgroups) the 16 x 4U outputs, clear acc.
+template <int U, int W>
+__device__ __forceinline__ void stream_tile_end(float (&acc)[U][4], float *red, int wave, int tid, int lane,
+                                                const TileRef &r, int64_t m0, int64_t M, int atomic)
+{
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float v = acc[u][k];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[u][k] = v;
+        }
+    if constexpr (W == 1) {
+        if (lane < 16) {
+            const int64_t n = r.lt * kTileRows + lane;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int64_t m = m0 + 4 * u + k;
+                    if (m < M && n < r.n) {
+                        float *o = r.out + m * r.ldo + n;
+                        if (atomic)
+                            atomicAdd(o, acc[u][k]);
+                        else
+                            *o = acc[u][k];
+                    }
+                }
+        }
+    } else {
+        if (lane < 16) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    red[((wave * U + u) * 4 + k) * 16 + lane] = acc[u][k];
+        }
+        __syncthreads();
+        for (int i = tid; i < U * 64; i += W * 64) {
+            const int u = i >> 6, k = (i >> 4) & 3, c = i & 15;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; ++w)
+                v += red[((w * U + u) * 4 + k) * 16 + c];
+            const int64_t m = m0 + 4 * u + k, n = r.lt * kTileRows + c;
+            if (m < M && n < r.n) {
+                float *o = r.out + m * r.ldo + n;
+                if (atomic)
+                    atomicAdd(o, v);
+                else
+                    *o = v;
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            acc[u][k] = 0.0f;
+}
+
+// Workgroup (x, y, z) computes tiles [x*tpw, x*tpw + tpw) of the launch over K blocks
+// [y*bps, y*bps + bps) for tokens [16z, 16z + 4U). Its W waves split each tile's blocks
+// (wave w takes blocks w, w + W, ...) and stream the tiles back to back through one
+// register ring, so the ring does not drain between tiles and the activations are
+// staged in LDS once per workgroup.
 template <int U, int W, bool kLdsAct>
 __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
-                                                             GroupArgs ga, int B, int bps, int atomic)
+                                                             GroupArgs ga, int64_t ntiles, int tpw, int B, int bps,
+                                                             int atomic)
 {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -209,28 +324,27 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     const int64_t m0 = (int64_t)blockIdx.z * 16;
     const int rows = (int)min<int64_t>(U * 4, M - m0);
     const StreamLds L = stream_lds(U, W, rows, K, kLdsAct);
-    // This workgroup's projection (constant indices only, so the arguments stay scalar).
-    const uint8_t *packed = ga.packed[0];
-    float *out = ga.out[0];
-    int64_t N = ga.n[0], ldo = ga.ldo[0], t = blockIdx.x;
-#pragma unroll
-    for (int g = 1; g < kMaxGroup; ++g)
-        if (g < ga.count && (int64_t)blockIdx.x >= ga.tile_begin[g]) {
-            packed = ga.packed[g];
-            out = ga.out[g];
-            N = ga.n[g];
-            ldo = ga.ldo[g];
-            t = blockIdx.x - ga.tile_begin[g];
-        }
+    const int64_t t_begin = (int64_t)blockIdx.x * tpw;
+    const int ntw = (int)min<int64_t>(tpw, ntiles - t_begin);
     const int b_begin = blockIdx.y * bps;
     const int b_end = min(B, b_begin + bps);
-    const int col = lane & 15, q = lane >> 4;
-    const uint8_t *wt = packed + t * (int64_t)B * kTileBytes;
-    // Blocks of this wave: first, first + W, ... (count is wave-uniform).
+    // steps per tile, the same for every wave (blocks past b_end count with a zero scale)
+    const int steps = (b_end - b_begin + W - 1) / W;
+    const int total = ntw * steps;
     const int first = b_begin + wave;
-    const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
-    const int last = first + (count - 1) * W;
+    const int col = lane & 15, q = lane >> 4;
+
+    // Ring of kDepth register sets with fixed slots (the loop body is unrolled kDepth
+    // times): step s is decoded while steps s+1 .. s+kDepth-1 are in flight. The first
+    // loads go out before the activations are staged.
     WTile wr[kDepth];
+    StreamCursor pc = {0, 0, t_begin, tile_ref(ga, t_begin, B).w};
+#pragma unroll
+    for (int j = 0; j < kDepth - 1; ++j) {
+        wr[j] = load_w(pc.w + (int64_t)min(first + pc.i * W, b_end - 1) * kTileBytes, lane, col);
+        advance(pc, total, steps, ga, B);
+    }
+
     __shared__ uint32_t s_grid[512];
     const uint8_t *lut = reinterpret_cast<const uint8_t *>(s_grid);
     {
@@ -284,105 +398,55 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
         for (int r = 0; r < 4; ++r)
             acc[u][r] = 0.0f;
 
-    // A ring of kDepth register sets with fixed slots (the loop body is unrolled kDepth
-    // times): block i is decoded while blocks i+1 .. i+kDepth-1 are in flight. Prefetch
-    // addresses are clamped to the wave's last block and blocks past the end get a zero
-    // group scale, so the body has no branches and every load stays ahead of its use.
     // Activations staged in LDS are read at decode time; otherwise they ride in the ring
-    // with the weights.
-    if (count > 0) {
+    // with the weights (the first kDepth-1 of them are read here, after the staging).
+    ATile<U> ar[kLdsAct ? 1 : kDepth];
+    if constexpr (!kLdsAct) {
+        StreamCursor ac = {0, 0, t_begin, nullptr};
 #pragma unroll
-        for (int j = 0; j < kDepth - 1; ++j)
-            wr[j] = load_w(wt + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
-        ATile<U> ar[kLdsAct ? 1 : kDepth];
-        if constexpr (!kLdsAct) {
-#pragma unroll
-            for (int j = 0; j < kDepth - 1; ++j)
-                load_a<U>(ar[j], al, min(first + j * W, last));
-        }
-        for (int i0 = 0; i0 < count; i0 += kDepth) {
-#pragma unroll
-            for (int j = 0; j < kDepth; ++j) {
-                const int i = i0 + j;
-                const int slot = (j + kDepth - 1) % kDepth;
-                const int bp = min(first + (i + kDepth - 1) * W, last);
-                wr[slot] = load_w(wt + (int64_t)bp * kTileBytes, lane, col);
-                if constexpr (!kLdsAct)
-                    load_a<U>(ar[slot], al, bp);
-                // keep the prefetch issued before the decode of block i (scheduler fence)
-                if constexpr (MAMBO_SCHED_FENCE)
-                    __builtin_amdgcn_sched_barrier(0);
-                // blocks past the wave's range (the ring's tail) skip the math; the branch
-                // is wave-uniform and the loads above stay unconditional
-                if (i < count) {
-                    if constexpr (kLdsAct) {
-                        load_a<U>(ar[0], al, min(first + i * W, last));
-                        compute_block<U>(wr[j], ar[0], lut, acc, i < count);
-                    } else {
-                        compute_block<U>(wr[j], ar[j], lut, acc, i < count);
-                    }
-                }
-                if constexpr (MAMBO_SCHED_FENCE)
-                    __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < kDepth - 1; ++j) {
+            load_a<U>(ar[j], al, min(first + ac.i * W, b_end - 1));
+            if (ac.s + 1 < total) {
+                ++ac.s;
+                if (++ac.i == steps)
+                    ac.i = 0;
             }
         }
     }
-
-    if constexpr (W == 1) {
-        // sum the four K chunks (lanes col, col+16, col+32, col+48) within the wave
+    float *red = reinterpret_cast<float *>(smem + L.red);
+    int ci = 0, tile_no = 0; // step within the tile being decoded, and its index in the run
+    for (int s0 = 0; s0 < total; s0 += kDepth) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = acc[u][r];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
-                acc[u][r] = v;
-            }
-        if (lane < 16) {
-            const int64_t n = t * kTileRows + lane;
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t m = m0 + 4 * u + r;
-                    if (m < M && n < N) {
-                        float *o = out + m * ldo + n;
-                        if (atomic)
-                            atomicAdd(o, acc[u][r]);
-                        else
-                            *o = acc[u][r];
-                    }
+        for (int j = 0; j < kDepth; ++j) {
+            const int s = s0 + j;
+            const int slot = (j + kDepth - 1) % kDepth;
+            const int bp = min(first + pc.i * W, b_end - 1);
+            wr[slot] = load_w(pc.w + (int64_t)bp * kTileBytes, lane, col);
+            if constexpr (!kLdsAct)
+                load_a<U>(ar[slot], al, bp);
+            advance(pc, total, steps, ga, B);
+            // keep the prefetch issued before the decode of step s (scheduler fence)
+            if constexpr (MAMBO_SCHED_FENCE)
+                __builtin_amdgcn_sched_barrier(0);
+            // steps past the run (the ring's tail) skip the math; the condition is uniform
+            // over the workgroup, so the tile-end barrier inside is reached by every wave
+            if (s < total) {
+                const int blk = first + ci * W;
+                if constexpr (kLdsAct) {
+                    load_a<U>(ar[0], al, min(blk, b_end - 1));
+                    compute_block<U>(wr[j], ar[0], lut, acc, blk < b_end);
+                } else {
+                    compute_block<U>(wr[j], ar[j], lut, acc, blk < b_end);
                 }
-        }
-    } else {
-        // cross-wave sum through LDS, one 4-row sub-tile at a time
-        float *red = reinterpret_cast<float *>(smem + L.red);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (u > 0)
-                __syncthreads();
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                red[(wave * 4 + r) * 64 + lane] = acc[u][r];
-            __syncthreads();
-            for (int i = tid; i < 4 * 16; i += W * 64) {
-                const int r = i >> 4, c = i & 15;
-                float v = 0.0f;
-#pragma unroll
-                for (int w = 0; w < W; ++w)
-#pragma unroll
-                    for (int qq = 0; qq < 4; ++qq)
-                        v += red[(w * 4 + r) * 64 + qq * 16 + c];
-                const int64_t m = m0 + 4 * u + r, n = t * kTileRows + c;
-                if (m < M && n < N) {
-                    float *o = out + m * ldo + n;
-                    if (atomic)
-                        atomicAdd(o, v);
-                    else
-                        *o = v;
+                if (++ci == steps) {
+                    stream_tile_end<U, W>(acc, red + (tile_no & 1) * (W * U * 64), wave, tid, lane,
+                                          tile_ref(ga, t_begin + tile_no, B), m0, M, atomic);
+                    ci = 0;
+                    ++tile_no;
                 }
             }
+            if constexpr (MAMBO_SCHED_FENCE)
+                __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
@@ -905,35 +969,43 @@ __global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t 
     (void)rows;
 }
 
+// Launch arguments of the stream kernel beyond the operands.
+struct StreamLaunch {
+    dim3 grid;
+    size_t lds;
+    int64_t ntiles; // 16-row tiles of the launch (all projections)
+    int tpw;        // tiles per workgroup
+    int B, bps, atomic;
+};
+
 template <int U, int W, bool kLdsAct>
-void launch_stream_uwa(dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
-                       int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+void launch_stream_uwa(const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
+                       int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
-    hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
-                       ga, B, bps, atomic);
+    hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs, ldxs,
+                       M, ga, sl.ntiles, sl.tpw, sl.B, sl.bps, sl.atomic);
 }
 
 template <int U, int W>
-void launch_stream_uw(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                      const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+void launch_stream_uw(bool lds_act, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                      const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
     if (lds_act)
-        launch_stream_uwa<U, W, true>(grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+        launch_stream_uwa<U, W, true>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
     else
-        launch_stream_uwa<U, W, false>(grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+        launch_stream_uwa<U, W, false>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
 }
 
 // Waves per workgroup the stream kernel is built for.
 constexpr int kStreamWaves[] = {1, 2, 4, 6, 8, 12, 16};
 
 template <int U>
-int launch_stream_u(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
-                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
-                    int atomic)
+int launch_stream_u(int waves, bool lds_act, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv,
+                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_stream_uw<U, WV>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);             \
+        launch_stream_uw<U, WV>(lds_act, sl, stream, xv, ldxv, xs, ldxs, M, ga);                                     \
         break;
     switch (waves) {
         MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
@@ -1025,6 +1097,8 @@ constexpr int kMaxLdsAct = MAMBO_MAX_LDS_ACT_KB * 1024;
 // Compute units of an MI355X (the tiled default sizes its grid to at least one
 // workgroup per CU).
 constexpr int64_t kCUs = 256;
+// Workgroups the stream kernel's default aims for when it has many tiles.
+constexpr int64_t kStreamWgs = 512;
 // Token count from which the default configuration uses the tiled kernel.
 constexpr int64_t kTiledMinM = 64;
 // Dynamic LDS per workgroup (the static codebook tables add 2.3 KiB).
@@ -1114,6 +1188,13 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
                 waves = w;
         units = cdiv(rt, nt) * cdiv(m, 16);
     }
+    if (c.kernel == MAMBO_GEMM_STREAM) {
+        // Runs of tiles per workgroup: about two workgroups per CU (512) walking their
+        // tiles back to back beat one short-lived workgroup per tile once there are
+        // several tiles per CU (measured on gfx950 at M = 1 and 4: 7 tiles per workgroup
+        // for 3584 tiles, 4 for 1792, 1 for 512-640).
+        c.tile_n = (int32_t)(kTileRows * std::max<int64_t>(1, (units + kStreamWgs / 2) / kStreamWgs));
+    }
     int64_t split = 1;
     if (units * waves < (c.kernel == MAMBO_GEMM_DENSE ? kMinWaves / 4 : kMinWaves)) {
         const int64_t per_split_waves = units * waves;
@@ -1154,6 +1235,9 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
     if (cfg->kernel == MAMBO_GEMM_DENSE)
         MAMBO_REQUIRE(cfg->tile_n == 0 || cfg->tile_n == 16 || cfg->tile_n == 32 || cfg->tile_n == 64,
                       MAMBO_ERR_VALUE, "dense: tile_n must be 16, 32 or 64 weight rows");
+    else
+        MAMBO_REQUIRE(cfg->tile_n >= 0 && cfg->tile_n % kTileRows == 0 && cfg->tile_n <= (1 << 20), MAMBO_ERR_VALUE,
+                      "stream: tile_n must be a multiple of 16 weight rows, at most 2^20");
     MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                   "split_k must be in [1, K/256]");
     return MAMBO_OK;
@@ -1274,11 +1358,14 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
                       "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
                       c.waves, (long long)m);
+        const int tpw = (int)std::min<int64_t>(c.tile_n ? c.tile_n / kTileRows : 1, tiles);
+        StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic};
+        sl.grid.x = (unsigned)cdiv(tiles, tpw);
         switch (U) {
-        case 1: rc = launch_stream_u<1>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
-        case 2: rc = launch_stream_u<2>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
-        case 3: rc = launch_stream_u<3>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
-        default: rc = launch_stream_u<4>(c.waves, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, ga, B, bps, atomic); break;
+        case 1: rc = launch_stream_u<1>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        case 2: rc = launch_stream_u<2>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        case 3: rc = launch_stream_u<3>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        default: rc = launch_stream_u<4>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
         }
     }
     if (rc)

@@ -58,13 +58,18 @@ def test_gemm_config_defaults_and_validation():
     assert lib.mambo_gemm_default_config(1, 4096, 16, ctypes.byref(cfg)) == 0
     assert cfg.kernel == _native.GEMM_STREAM and cfg.waves in (1, 2, 4, 6, 8, 12, 16) and 1 <= cfg.split_k <= 16
     # 8 waves with at least 4 blocks each (or small grids), 4 for large grids of short K,
-    # 16 for tiny grids, K split only below 512 waves
-    for n, blocks, waves, split in ((28672, 32, 8, 1), (8192, 32, 8, 1), (8192, 112, 8, 1), (10240, 32, 8, 1),
-                                    (57344, 32, 8, 1), (28672, 16, 4, 1), (4096, 16, 8, 1), (1024, 32, 16, 1),
-                                    (1024, 16, 8, 1), (64, 64, 16, 2)):
+    # 16 for tiny grids, K split only below 512 waves; runs of round(tiles / 512) tiles
+    # per workgroup (tile_n = 16 rows per tile)
+    for n, blocks, waves, split, tile_n in (
+            (28672, 32, 8, 1, 64), (8192, 32, 8, 1, 16), (8192, 112, 8, 1, 16), (10240, 32, 8, 1, 16),
+            (57344, 32, 8, 1, 112), (28672, 16, 4, 1, 64), (4096, 16, 8, 1, 16), (1024, 32, 16, 1, 16),
+            (1024, 16, 8, 1, 16), (64, 64, 16, 2, 16), (14336, 16, 8, 1, 32)):
         big = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(1, n, blocks, ctypes.byref(big)) == 0
-        assert (big.waves, big.split_k) == (waves, split), (n, blocks, big.as_dict())
+        assert (big.waves, big.split_k, big.tile_n) == (waves, split, tile_n), (n, blocks, big.as_dict())
+    for tile_n, rc in ((0, 0), (48, 0), (16 * 4096, 0), (24, _native.MAMBO_ERR_VALUE), (-16, _native.MAMBO_ERR_VALUE)):
+        c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 1, "tile_n": tile_n})
+        assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(c)) == rc, tile_n
     bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 5, "split_k": 1})
     assert lib.mambo_gemm_check_config(1, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE
     bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 9})

@@ -231,6 +231,40 @@ def test_grouped_projections_match_single_launches(gpu, m):
             check(o.cpu().numpy(), e)
 
 
+@pytest.mark.parametrize("m", [1, 3, 4, 9])
+def test_stream_kernel_multi_tile_runs(gpu, m):
+    """Stream kernel workgroups that walk a run of row tiles: runs of 1..14 tiles over a
+    grouped launch whose projections (N = 100, 37, 64: 7 + 3 + 4 tiles, the last of each
+    partial) make runs cross projection boundaries and leave the last run short; more
+    waves than K blocks (idle waves), and a K split over workgroups. Every run length
+    gives the same bits as one tile per workgroup (same summation order) and matches the
+    oracle."""
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul_grouped
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    k = 2048
+    raws = [make_synthetic_iq3_s(n, k, seed=140 + i) for i, n in enumerate((100, 37, 64))]
+    fields = [prepare_iq3_s_fields(torch.from_numpy(r).to(gpu)) for r in raws]
+    x = np.random.default_rng(11 + m).standard_normal((m, k)).astype(np.float32)
+    xv, xs = oracle.quantize_mxfp8(x)
+    xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+    expected = [oracle.iq3s_fp8_matmul(xv, xs, r) for r in raws]
+    for waves in (1, 4, 8, 16):
+        for split in (1, 3):
+            base = None
+            for tiles_per_wg in (1, 2, 3, 5, 14, 20):
+                cfg = {"kernel": _native.GEMM_STREAM, "waves": waves, "split_k": split, "tile_n": 16 * tiles_per_wg}
+                step(f"stream multi-tile M={m} N=100+37+64 K=2048 cfg={cfg}")
+                outs = [o.cpu().numpy() for o in launch_iq3_s_fp8_matmul_grouped(xvg, xsg, fields, config=cfg)]
+                for o, e in zip(outs, expected):
+                    check(o, e)
+                if split == 1:
+                    if base is None:
+                        base = outs
+                    for o, b in zip(outs, base):
+                        np.testing.assert_array_equal(o, b)
+
+
 def test_grouped_into_strided_outputs(gpu):
     from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul_grouped
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
