@@ -71,6 +71,30 @@ __device__ __forceinline__ WTile load_w(const uint8_t *__restrict__ tb, uint32_t
     return w;
 }
 
+// Buffer resource over the 4 GiB that start at `base` (raw, unswizzled): loads through
+// it take a scalar base, a 32-bit lane offset, a scalar step offset and an immediate
+// field offset, with no per-lane 64-bit address arithmetic. The host keeps every offset
+// below 2^32 (run_projections checks the activation strides; weight offsets are at most
+// K/256 * 1760 bytes per tile).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_rsrc(const void *base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)0xFFFFFFFFu, 0x00020000);
+}
+
+// load_w through a buffer resource: the tile at byte `step` past the resource base.
+__device__ __forceinline__ WTile load_w_rsrc(__amdgpu_buffer_rsrc_t r, uint32_t step, uint32_t lane, uint32_t col)
+{
+    WTile w;
+    const auto ia = __builtin_amdgcn_raw_buffer_load_b128(r, 16u * lane + kTileIdxA, step, 0);
+    w.ia = uint4{ia[0], ia[1], ia[2], ia[3]};
+    w.ib = __builtin_amdgcn_raw_buffer_load_b16(r, 2u * lane + kTileIdxB, step, 0);
+    const auto sg = __builtin_amdgcn_raw_buffer_load_b64(r, 8u * lane + kTileSigns, step, 0);
+    w.sg = uint2{sg[0], sg[1]};
+    w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, lane + kTileScales, step, 0);
+    w.dh = __builtin_amdgcn_raw_buffer_load_b16(r, 2u * col + kTileD, step, 0);
+    return w;
+}
+
 // Byte address (idx << 2) of code I's grid word; idx = bits [9I, 9I+9) of the stream.
 template <int I>
 __device__ __forceinline__ uint32_t code_addr(const uint32_t (&s)[5])
@@ -222,11 +246,12 @@ __device__ __forceinline__ TileRef tile_ref(const GroupArgs &ga, int64_t t, int 
 }
 
 // Position of a wave in its workgroup's run of (tile, step) pairs: step i of a tile is
-// super-block first + i*W; `w` is the tile's first super-block.
+// super-block first + i*W; `w` is a buffer resource starting at the tile's first
+// super-block.
 struct StreamCursor {
     int s, i;
     int64_t t;
-    const uint8_t *w;
+    __amdgpu_buffer_rsrc_t w;
 };
 
 // Move to the next pair unless at the last one (the ring's tail keeps re-reading it).
@@ -237,7 +262,7 @@ __device__ __forceinline__ void advance(StreamCursor &c, int total, int steps, c
         if (++c.i == steps) {
             c.i = 0;
             ++c.t;
-            c.w = tile_ref(ga, c.t, B).w;
+            c.w = byte_rsrc(tile_ref(ga, c.t, B).w);
         }
     }
 }
@@ -338,10 +363,10 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     // times): step s is decoded while steps s+1 .. s+kDepth-1 are in flight. The first
     // loads go out before the activations are staged.
     WTile wr[kDepth];
-    StreamCursor pc = {0, 0, t_begin, tile_ref(ga, t_begin, B).w};
+    StreamCursor pc = {0, 0, t_begin, byte_rsrc(tile_ref(ga, t_begin, B).w)};
 #pragma unroll
     for (int j = 0; j < kDepth - 1; ++j) {
-        wr[j] = load_w(pc.w + (int64_t)min(first + pc.i * W, b_end - 1) * kTileBytes, lane, col);
+        wr[j] = load_w_rsrc(pc.w, (uint32_t)min(first + pc.i * W, b_end - 1) * kTileBytes, lane, col);
         advance(pc, total, steps, ga, B);
     }
 
@@ -402,14 +427,14 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     // with the weights (the first kDepth-1 of them are read here, after the staging).
     ATile<U> ar[kLdsAct ? 1 : kDepth];
     if constexpr (!kLdsAct) {
-        StreamCursor ac = {0, 0, t_begin, nullptr};
+        int as = 0, ai = 0; // the prefetch cursor's (s, i) for these first steps
 #pragma unroll
         for (int j = 0; j < kDepth - 1; ++j) {
-            load_a<U>(ar[j], al, min(first + ac.i * W, b_end - 1));
-            if (ac.s + 1 < total) {
-                ++ac.s;
-                if (++ac.i == steps)
-                    ac.i = 0;
+            load_a<U>(ar[j], al, min(first + ai * W, b_end - 1));
+            if (as + 1 < total) {
+                ++as;
+                if (++ai == steps)
+                    ai = 0;
             }
         }
     }
@@ -421,7 +446,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
             const int s = s0 + j;
             const int slot = (j + kDepth - 1) % kDepth;
             const int bp = min(first + pc.i * W, b_end - 1);
-            wr[slot] = load_w(pc.w + (int64_t)bp * kTileBytes, lane, col);
+            wr[slot] = load_w_rsrc(pc.w, (uint32_t)bp * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
                 load_a<U>(ar[slot], al, bp);
             advance(pc, total, steps, ga, B);
@@ -491,6 +516,20 @@ __device__ __forceinline__ void load_a_dense(ADense &at, const uint8_t *__restri
     }
 }
 
+// load_a_dense from global memory through buffer resources over the chunk's activation
+// rows (xr) and scales (sr).
+__device__ __forceinline__ void load_a_dense_rsrc(ADense &at, __amdgpu_buffer_rsrc_t xr, uint32_t xoff,
+                                                  __amdgpu_buffer_rsrc_t sr, uint32_t soff, int b)
+{
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const auto lo = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 32u * h, 256u * b, 0);
+        const auto hi = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 32u * h + 64u, 256u * b, 0);
+        at.a[h] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        at.s[h] = __builtin_amdgcn_raw_buffer_load_b8(sr, soff + h, 8u * b, 0);
+    }
+}
+
 // hi and lo words of code C of a group: level bytes select from the split table entry
 // (tab.x/.y: hi of levels 0-3/4-7, tab.z/.w: lo); the four signs, moved onto bits
 // 7,15,23,31 by one shift of the transposed sign word, are OR-ed into hi and XOR-ed into
@@ -539,13 +578,13 @@ __device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, 
     to_dense_order(l0);
     to_dense_order(h1);
     to_dense_order(l1);
-    // B scale 2^1: the split terms are stored halved
+    // B scale 2^1: the split terms are stored halved.
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
-    v4f c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
-    c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c1, 0, 0, 0, (int)at.s[1], 0, 128);
-    c2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c2, 0, 0, 0, (int)at.s[1], 0, 128);
-    const v4f c = c1 + c2;
+    // one chain of four MFMAs: the callers interleave the chains of their NT tiles
+    v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, c, 0, 0, 0, (int)at.s[0], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c, 0, 0, 0, (int)at.s[1], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c, 0, 0, 0, (int)at.s[1], 0, 128);
     const float f = valid ? half_bits_to_float((uint16_t)w.dh) : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -602,10 +641,10 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     const int b_begin = blockIdx.y * bps;
     const int b_end = min(B, b_begin + bps);
     const int col = lane & 15, q = lane >> 4;
-    const uint8_t *wt[NT];
+    __amdgpu_buffer_rsrc_t wt[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) // tiles past the weight's last are clamped; stores are masked
-        wt[nt] = packed + min(wg * NT + nt, tiles - 1) * (int64_t)B * kTileBytes;
+        wt[nt] = byte_rsrc(packed + min(wg * NT + nt, tiles - 1) * (int64_t)B * kTileBytes);
     const int first = b_begin + wave;
     const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
     const int last = first + (count - 1) * W;
@@ -637,16 +676,13 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     // M read the chunk's last token: they only feed output rows that are never stored.
     const int rowc = min(col, rows - 1);
     const uint32_t xo = 32u * (4 * (q >> 1)) + 16u * (q & 1), so = 4u * (q & 1) + 2u * (q >> 1);
-    const uint8_t *xbase, *sbase;
+    const uint8_t *xbase = smem + L.x, *sbase = smem + L.xs;     // kLdsAct
+    __amdgpu_buffer_rsrc_t xr = byte_rsrc(xv + m0 * ldxv), sr = byte_rsrc(xs + m0 * ldxs); // otherwise
     uint32_t xoff, soff;
     if constexpr (kLdsAct) {
-        xbase = smem + L.x;
-        sbase = smem + L.xs;
         xoff = (uint32_t)(rowc * K) + xo;
         soff = (uint32_t)(rowc * (K / 32)) + so;
     } else {
-        xbase = xv + m0 * ldxv;
-        sbase = xs + m0 * ldxs;
         xoff = (uint32_t)(rowc * ldxv) + xo;
         soff = (uint32_t)(rowc * ldxs) + so;
     }
@@ -664,9 +700,9 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         for (int j = 0; j < kDepth - 1; ++j) {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
-                wr[j][nt] = load_w(wt[nt] + (int64_t)min(first + j * W, last) * kTileBytes, lane, col);
+                wr[j][nt] = load_w_rsrc(wt[nt], (uint32_t)min(first + j * W, last) * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
-                load_a_dense(ar[j], xbase, xoff, sbase, soff, min(first + j * W, last));
+                load_a_dense_rsrc(ar[j], xr, xoff, sr, soff, min(first + j * W, last));
         }
         for (int i0 = 0; i0 < count; i0 += kDepth) {
 #pragma unroll
@@ -676,9 +712,9 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                 const int bp = min(first + (i + kDepth - 1) * W, last);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
-                    wr[slot][nt] = load_w(wt[nt] + (int64_t)bp * kTileBytes, lane, col);
+                    wr[slot][nt] = load_w_rsrc(wt[nt], (uint32_t)bp * kTileBytes, lane, col);
                 if constexpr (!kLdsAct)
-                    load_a_dense(ar[slot], xbase, xoff, sbase, soff, bp);
+                    load_a_dense_rsrc(ar[slot], xr, xoff, sr, soff, bp);
                 if constexpr (MAMBO_SCHED_FENCE)
                     __builtin_amdgcn_sched_barrier(0);
                 if constexpr (kLdsAct)
@@ -839,12 +875,12 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     const int64_t tiles = (N + kTileRows - 1) / kTileRows;
     const int64_t m0 = (int64_t)blockIdx.y * kRows;
     // weight tiles of this wave (clamped to the last tile; stores are masked)
-    const uint8_t *wt[NT];
+    __amdgpu_buffer_rsrc_t wt[NT];
     int64_t tile[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         tile[nt] = wg * (NT * W) + wave * NT + nt;
-        wt[nt] = packed + min(tile[nt], tiles - 1) * (int64_t)B * kTileBytes;
+        wt[nt] = byte_rsrc(packed + min(tile[nt], tiles - 1) * (int64_t)B * kTileBytes);
     }
 
     for (int i = tid; i < 512; i += kThreads)
@@ -856,7 +892,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     // thread tid owns chunks tid + j*kThreads.
     uint4 stage[kPerThread];
     uint2 sstage = {0u, 0u};
-    const uint8_t *xtile = xv + m0 * ldxv; // chunk rows past M are clamped to row M-1
+    const __amdgpu_buffer_rsrc_t xtile = byte_rsrc(xv + m0 * ldxv); // rows past M are clamped to row M-1
     const int64_t last_row = M - 1 - m0;
     // scales: thread tid stages row min(tid, kRows-1); the threads past kRows rewrite the
     // last row's identical bytes, which keeps the staging branch-free
@@ -867,8 +903,9 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     constexpr auto kJ = std::make_integer_sequence<int, kPerThread>{};
     auto load_one = [&](int j, int b) -> uint4 {
         const int c = min(tid + j * kThreads, kChunks - 1);
-        return *reinterpret_cast<const uint4 *>(xtile + min<int64_t>(c >> 4, last_row) * ldxv +
-                                                (256 * (int64_t)b + 16 * (c & 15)));
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+            xtile, (uint32_t)min<int64_t>(c >> 4, last_row) * (uint32_t)ldxv + 16u * (c & 15), 256u * b, 0);
+        return uint4{v[0], v[1], v[2], v[3]};
     };
     auto store_one = [&](int j, int buf, uint4 v) {
         const int c = tid + j * kThreads;
@@ -913,7 +950,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     float d[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-        wcur[nt] = load_w(wt[nt] + (int64_t)b0 * kTileBytes, lane, col);
+        wcur[nt] = load_w_rsrc(wt[nt], (uint32_t)b0 * kTileBytes, lane, col);
     MAMBO_LOAD_STAGE(b0);
     MAMBO_STORE_STAGE(b0 & 1);
     MAMBO_LOAD_STAGE(min(b0 + 1, b1 - 1));
@@ -926,7 +963,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
         MAMBO_LOAD_STAGE(min(b + 2, b1 - 1));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-            wnext[nt] = load_w(wt[nt] + (int64_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);
+            wnext[nt] = load_w_rsrc(wt[nt], (uint32_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);
         __builtin_amdgcn_sched_barrier(0);
         decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);
         mfma_block<MT, NT>(smem + (b & 1) * kABytes + aoff, smem + 2 * kABytes + (b & 1) * kSBytes + soff, bh, bl, d,
@@ -1257,7 +1294,8 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     MAMBO_REQUIRE(blocks <= (1 << 20), MAMBO_ERR_VALUE, "K too large");
     const int64_t k = blocks * 256;
     MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32, MAMBO_ERR_VALUE, "activation row strides must cover the row");
-    MAMBO_REQUIRE(ldxv < ((int64_t)1 << 27), MAMBO_ERR_VALUE, "activation row stride too large");
+    MAMBO_REQUIRE(ldxv < ((int64_t)1 << 27) && ldxs < ((int64_t)1 << 27), MAMBO_ERR_VALUE,
+                  "activation row stride too large");
     MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
                   "x_values base and row stride must be 16-byte aligned");
     GroupArgs ga = {};
@@ -1313,6 +1351,9 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);
         MAMBO_REQUIRE((uintptr_t)xs % 8 == 0 && ldxs % 8 == 0, MAMBO_ERR_VALUE,
                       "tiled: x_scales base and row stride must be 8-byte aligned");
+        // the staging loads address a token tile with 32-bit offsets
+        MAMBO_REQUIRE((int64_t)c.tile_m * ldxv < ((int64_t)1 << 32), MAMBO_ERR_VALUE,
+                      "tiled: activation row stride too large for tile_m=%d", c.tile_m);
         // workgroups per projection; tile_begin counts workgroups for this kernel
         GroupArgs gt = ga;
         int64_t wgs = 0;
