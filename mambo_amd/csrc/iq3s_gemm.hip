@@ -694,36 +694,73 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         for (int r = 0; r < 4; ++r)
             acc[nt][r] = 0.0f;
     if (count > 0) {
-        WTile wr[kDepth][NT];
-        ADense ar[kLdsAct ? 1 : kDepth];
-#pragma unroll
-        for (int j = 0; j < kDepth - 1; ++j) {
+        if constexpr (NT >= 4) {
+            // Per tile: decode step i's block, then reload the same registers with step
+            // i+1's block, so the next step's NT blocks are in flight during this step's
+            // decodes while only one block per tile is held (the activation fragments keep
+            // a ring of two). With four tiles that is a step of prefetch distance in half
+            // the registers of a two-step ring (occupancy 3 instead of 2, measured faster);
+            // with fewer tiles the distance gets too short and the two-step ring is used.
+            WTile wr[NT];
+            ADense ar[kLdsAct ? 1 : 2];
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
-                wr[j][nt] = load_w_rsrc(wt[nt], (uint32_t)min(first + j * W, last) * kTileBytes, lane, col);
+                wr[nt] = load_w_rsrc(wt[nt], (uint32_t)first * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
-                load_a_dense_rsrc(ar[j], xr, xoff, sr, soff, min(first + j * W, last));
-        }
-        for (int i0 = 0; i0 < count; i0 += kDepth) {
+                load_a_dense_rsrc(ar[0], xr, xoff, sr, soff, first);
+            for (int i0 = 0; i0 < count; i0 += 2) {
 #pragma unroll
-            for (int j = 0; j < kDepth; ++j) {
-                const int i = i0 + j;
-                const int slot = (j + kDepth - 1) % kDepth;
-                const int bp = min(first + (i + kDepth - 1) * W, last);
+                for (int j = 0; j < 2; ++j) {
+                    const int i = i0 + j;
+                    const int bn = min(first + (i + 1) * W, last);
+                    if constexpr (!kLdsAct)
+                        load_a_dense_rsrc(ar[j ^ 1], xr, xoff, sr, soff, bn);
+                    else
+                        load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        if constexpr (MAMBO_SCHED_FENCE)
+                            __builtin_amdgcn_sched_barrier(0);
+                        compute_dense(wr[nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
+                        wr[nt] = load_w_rsrc(wt[nt], (uint32_t)bn * kTileBytes, lane, col);
+                    }
+                    if constexpr (MAMBO_SCHED_FENCE)
+                        __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else {
+            // Two-step ring: step i+1's blocks and activations load while step i decodes.
+            WTile wr[kDepth][NT];
+            ADense ar[kLdsAct ? 1 : kDepth];
+#pragma unroll
+            for (int j = 0; j < kDepth - 1; ++j) {
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
-                    wr[slot][nt] = load_w_rsrc(wt[nt], (uint32_t)bp * kTileBytes, lane, col);
+                    wr[j][nt] = load_w_rsrc(wt[nt], (uint32_t)min(first + j * W, last) * kTileBytes, lane, col);
                 if constexpr (!kLdsAct)
-                    load_a_dense_rsrc(ar[slot], xr, xoff, sr, soff, bp);
-                if constexpr (MAMBO_SCHED_FENCE)
-                    __builtin_amdgcn_sched_barrier(0);
-                if constexpr (kLdsAct)
-                    load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
+                    load_a_dense_rsrc(ar[j], xr, xoff, sr, soff, min(first + j * W, last));
+            }
+            for (int i0 = 0; i0 < count; i0 += kDepth) {
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    compute_dense(wr[j][nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
-                if constexpr (MAMBO_SCHED_FENCE)
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int j = 0; j < kDepth; ++j) {
+                    const int i = i0 + j;
+                    const int slot = (j + kDepth - 1) % kDepth;
+                    const int bp = min(first + (i + kDepth - 1) * W, last);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        wr[slot][nt] = load_w_rsrc(wt[nt], (uint32_t)bp * kTileBytes, lane, col);
+                    if constexpr (!kLdsAct)
+                        load_a_dense_rsrc(ar[slot], xr, xoff, sr, soff, bp);
+                    if constexpr (MAMBO_SCHED_FENCE)
+                        __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (kLdsAct)
+                        load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        compute_dense(wr[j][nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
+                    if constexpr (MAMBO_SCHED_FENCE)
+                        __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     }
