@@ -309,16 +309,20 @@ def main(argv=None) -> int:
     _native.lib()
     log(f"device {torch.cuda.get_device_name(0)} ({_native.device_arch()})")
 
+    dtype = "fp8-e4m3 x iq3_s, f32 accumulate"
+    data = "synthetic (counter-based IQ3_S blocks, bf16 ~N(0,1) activations)"
     if args.workload == "copy":
         r = run_copy(args)
         metric = "plain device copy GB/s (HBM counter calibration)"
         workload = f"copy {COPY_BYTES} bytes"
         config = {"workload": workload}
+        dtype, data = "u8", "synthetic bytes"
     elif args.workload == "quant":
         r = run_quant(args)
         metric = "MXFP8 activation quantizer GB/s (bf16 [4096,4096] -> E4M3 + E8M0)"
         workload = "mxfp8 quantize bf16 [4096,4096], 0.1% x100 outliers, 8 rotated inputs"
         config = {"workload": workload, "m": 4096, "k": 4096}
+        dtype, data = "bf16 -> fp8-e4m3 + e8m0", "synthetic (bf16 ~N(0,1), 0.1% x100 outliers)"
     else:
         r = run_gemm(args)
         metric = ("fused IQ3_S x MXFP8 GEMM TFLOP/s vs MX-FP8 MFMA roofline" if args.m >= PREFILL_M else
@@ -355,8 +359,8 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8-e4m3 x iq3_s, f32 accumulate",
-        "data": "synthetic (counter-based IQ3_S blocks, bf16 ~N(0,1) activations)",
+        "dtype": dtype,
+        "data": data,
         "config": config,
         "roofline": roofline,
     }
