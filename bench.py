@@ -272,6 +272,68 @@ def run_copy(args):
             "per_launch_bytes": nbytes, "per_launch_us": ms * 1e3}
 
 
+def run_read(args):
+    """Plain read of COPY_BYTES with mambo_read_bytes: the read ceiling of this device for
+    a stream of 16-byte loads (checked against the XOR of the input)."""
+    import torch
+    from mambo_amd import _native
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device="cuda")
+    src.copy_(torch.arange(COPY_BYTES // 4, dtype=torch.int32, device="cuda") * 2654435761)
+    sink = torch.empty(_native.READ_SINK_WORDS, dtype=torch.int32, device="cuda")
+
+    def launch():
+        _native.check(_native.lib().mambo_read_bytes(src.data_ptr(), COPY_BYTES, sink.data_ptr(),
+                                                     _native.stream_handle(None)), "read")
+
+    for _ in range(args.warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        launch()
+    stop.record()
+    torch.cuda.synchronize()
+    import numpy as np
+    if int(np.bitwise_xor.reduce(sink.cpu().numpy())) != int(np.bitwise_xor.reduce(src.cpu().numpy())):
+        raise RuntimeError("read kernel returned a wrong checksum")
+    ms = start.elapsed_time(stop) / args.steps
+    return {"ms": ms, "value": COPY_BYTES / (ms * 1e-3) / 1e9, "step_bytes": COPY_BYTES, "launches": 1,
+            "per_launch_bytes": COPY_BYTES, "per_launch_us": ms * 1e3}
+
+
+MFMA_WORKGROUPS = 1024  # x 4 waves: 4 waves per SIMD on 256 CUs
+MFMA_ITERS = 20000
+
+
+def run_mfma(args):
+    """Scaled-MFMA (f8f6f4 16x16x128) throughput with mambo_mfma_peak: the on-device
+    check of the 5.0 PFLOP/s dense MX-FP8 figure (checked against the known sums)."""
+    import torch
+    from mambo_amd import _native
+    out = torch.empty(MFMA_WORKGROUPS * 256, dtype=torch.float32, device="cuda")
+
+    def launch():
+        _native.check(_native.lib().mambo_mfma_peak(MFMA_WORKGROUPS, MFMA_ITERS, out.data_ptr(),
+                                                    _native.stream_handle(None)), "mfma_peak")
+
+    for _ in range(args.warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        launch()
+    stop.record()
+    torch.cuda.synchronize()
+    if not bool((out == 4096.0 * MFMA_ITERS).all()):
+        raise RuntimeError("MFMA throughput kernel returned wrong sums")
+    ms = start.elapsed_time(stop) / args.steps
+    flops = MFMA_WORKGROUPS * 4 * MFMA_ITERS * 8 * 2 * 16 * 16 * 128
+    return {"ms": ms, "value": flops / (ms * 1e-3) / 1e12, "tflops": flops / (ms * 1e-3) / 1e12,
+            "step_flops": flops, "launches": 1, "per_launch_us": ms * 1e3}
+
+
 def measured_traffic(workload: str):
     """HBM bytes per launch of the dominant kernel for `workload`, from the committed
     counter summaries (profiles/traffic_*.json), or None when none matches."""
@@ -288,7 +350,8 @@ def main(argv=None) -> int:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--m", type=int, default=1, help="tokens per projection")
-    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy"], default="llama70b")
+    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy", "read", "mfma"],
+                   default="llama70b")
     p.add_argument("--layers", type=int, default=None, help="layers in the sweep (default 80 for llama70b, 32 for llama8b)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-group", action="store_true",
@@ -317,6 +380,18 @@ def main(argv=None) -> int:
         workload = f"copy {COPY_BYTES} bytes"
         config = {"workload": workload}
         dtype, data = "u8", "synthetic bytes"
+    elif args.workload == "read":
+        r = run_read(args)
+        metric = "plain device read GB/s (16-byte loads, read ceiling)"
+        workload = f"read {COPY_BYTES} bytes"
+        config = {"workload": workload}
+        dtype, data = "u8", "synthetic bytes"
+    elif args.workload == "mfma":
+        r = run_mfma(args)
+        metric = "scaled MFMA f8f6f4 16x16x128 TFLOP/s (device check of the MX-FP8 peak)"
+        workload = f"mfma_scale_f32_16x16x128_f8f6f4: {MFMA_WORKGROUPS} workgroups x 4 waves x {MFMA_ITERS} x 8 MFMAs"
+        config = {"workload": workload}
+        dtype, data = "fp8-e4m3 x fp8-e4m3, f32 accumulate", "constant operands"
     elif args.workload == "quant":
         r = run_quant(args)
         metric = "MXFP8 activation quantizer GB/s (bf16 [4096,4096] -> E4M3 + E8M0)"
@@ -335,7 +410,7 @@ def main(argv=None) -> int:
         config = {"workload": workload, "m": args.m, "projections_per_step": r["projections"],
                   "launches_per_step": r["launches"], "weight_gb": round(r["weight_bytes"] / 1e9, 3),
                   "tflops": round(r["tflops"], 3), "graph": not args.no_graph}
-    mfma_bound = args.workload in ("llama70b", "llama8b") and args.m >= PREFILL_M
+    mfma_bound = (args.workload in ("llama70b", "llama8b") and args.m >= PREFILL_M) or args.workload == "mfma"
     value = r["tflops"] if mfma_bound else r["value"]
     unit = "TFLOP/s" if mfma_bound else "GB/s"
     if mfma_bound:

@@ -189,6 +189,20 @@ int mambo_fill_f32(float *ptr, int64_t n, float value, mambo_stream_t stream);
  * WRITE_SIZE) that the kernels' traffic figures are scaled by. */
 int mambo_copy_bytes(const void *src, void *dst, int64_t bytes, mambo_stream_t stream);
 
+/* Diagnostic: read `bytes` (a multiple of 16, src 16-byte aligned) with 16-byte vector
+ * loads over a grid of MAMBO_READ_SINK_WORDS threads; thread t writes the XOR of the
+ * 32-bit words of the chunks t, t + MAMBO_READ_SINK_WORDS, ... to sink[t], so `sink`
+ * holds MAMBO_READ_SINK_WORDS uint32 and the XOR of all of them is the XOR of the input.
+ * The plain-read ceiling that the weight streams are compared with. */
+#define MAMBO_READ_SINK_WORDS (2048 * 256)
+int mambo_read_bytes(const void *src, int64_t bytes, uint32_t *sink, mambo_stream_t stream);
+
+/* Diagnostic: scaled-MFMA throughput on this device. `workgroups` x 4 waves each run
+ * `iters` rounds of eight independent v_mfma_scale_f32_16x16x128_f8f6f4 chains (2*16*16*128
+ * flops per MFMA); out must hold workgroups * 256 floats and receives 4096 * iters in
+ * every element. */
+int mambo_mfma_peak(int64_t workgroups, int iters, float *out, mambo_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

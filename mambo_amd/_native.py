@@ -92,7 +92,11 @@ SIGNATURES = {
     "mambo_e4m3_convert": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "mambo_fill_f32": (_i32, [_vp, _i64, ctypes.c_float, _vp]),
     "mambo_copy_bytes": (_i32, [_vp, _vp, _i64, _vp]),
+    "mambo_read_bytes": (_i32, [_vp, _i64, _vp, _vp]),
+    "mambo_mfma_peak": (_i32, [_i64, ctypes.c_int, _vp, _vp]),
 }
+
+READ_SINK_WORDS = 2048 * 256  # MAMBO_READ_SINK_WORDS
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()

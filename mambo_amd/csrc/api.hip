@@ -95,6 +95,68 @@ extern "C" int mambo_copy_bytes(const void *src, void *dst, int64_t bytes, mambo
     return mambo_check_launch("copy_bytes");
 }
 
+// Plain read: each thread XORs the 16-byte chunks i, i + stride, ... and writes its XOR
+// to sink[thread]. Grid of kReadWorkgroups x 256. One load per iteration: at any moment
+// the grid reads one contiguous span (measured 6.5 TB/s on 1 GB; four strided loads per
+// iteration measured 5.6 TB/s).
+constexpr int64_t kReadWorkgroups = MAMBO_READ_SINK_WORDS / 256;
+
+__global__ __launch_bounds__(256) void read_bytes_kernel(const uint4 *__restrict__ src, int64_t n16,
+                                                         uint32_t *__restrict__ sink)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t x = 0;
+    for (int64_t i = t; i < n16; i += stride) {
+        const uint4 v = src[i];
+        x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    sink[t] = x;
+}
+
+extern "C" int mambo_read_bytes(const void *src, int64_t bytes, uint32_t *sink, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(bytes >= 0 && bytes % 16 == 0, MAMBO_ERR_VALUE, "bytes must be a non-negative multiple of 16");
+    MAMBO_REQUIRE(sink != nullptr, MAMBO_ERR_VALUE, "sink must not be NULL");
+    MAMBO_REQUIRE(bytes == 0 || (src != nullptr && (uintptr_t)src % 16 == 0), MAMBO_ERR_VALUE,
+                  "src must be non-NULL and 16-byte aligned");
+    hipLaunchKernelGGL(read_bytes_kernel, dim3((unsigned)kReadWorkgroups), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4 *)src, bytes / 16, sink);
+    return mambo_check_launch("read_bytes");
+}
+
+// Scaled-MFMA throughput: every wave runs `iters` rounds of eight independent chains of
+// v_mfma_scale_f32_16x16x128_f8f6f4 on E4M3 1.0 operands with unit E8M0 scales (each
+// MFMA adds 128 to every accumulator element), then writes the sum of its 32
+// accumulator values per lane: 8 * 4 * 128 * iters.
+__global__ __launch_bounds__(256) void mfma_peak_kernel(int iters, float *__restrict__ out)
+{
+    const v8i one = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
+    v4f c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        c[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(one, one, c[j], 0, 0, 0, 127, 0, 127);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        s += (c[j][0] + c[j][1]) + (c[j][2] + c[j][3]);
+    out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+extern "C" int mambo_mfma_peak(int64_t workgroups, int iters, float *out, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(workgroups >= 1 && workgroups <= 65536, MAMBO_ERR_VALUE, "workgroups must be in [1, 65536]");
+    MAMBO_REQUIRE(iters >= 0 && iters <= (1 << 20), MAMBO_ERR_VALUE, "iters must be in [0, 2^20]");
+    MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
+    hipLaunchKernelGGL(mfma_peak_kernel, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
+    return mambo_check_launch("mfma_peak");
+}
+
 extern "C" int mambo_fill_f32(float *ptr, int64_t n, float value, mambo_stream_t stream)
 {
     MAMBO_REQUIRE(n >= 0, MAMBO_ERR_VALUE, "n must be >= 0");

@@ -1149,7 +1149,7 @@ int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const
         launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                          \
         return MAMBO_OK;                                                                                           \
     }
-    MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
+    MAMBO_T(16, 1, 8) MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
     MAMBO_T(4, 2, 8) MAMBO_T(4, 2, 4) MAMBO_T(4, 1, 8) MAMBO_T(4, 1, 4)
 #undef MAMBO_T
     return mambo_fail(MAMBO_ERR_VALUE, "tiled kernel: no build for tile_m=%d, tile_n=%d, waves=%d", 16 * mt,
@@ -1207,14 +1207,18 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
                                          : MAMBO_GEMM_TILED;
     if (c.kernel == MAMBO_GEMM_TILED) {
         // The largest tile that still gives every CU a workgroup (measured on gfx950:
-        // 128 tokens x 256 weight rows x 8 waves is fastest when the grid fills the chip;
+        // 256 tokens x 128 weight rows x 8 waves is fastest when the grid fills the chip,
+        // 4-8% ahead of 128 x 256 x 8 - each decoded weight tile serves 16 token sub-tiles;
         // then 64 x 128 x 8 and 64 x 64 x 4); when even the smallest leaves CUs idle, K
         // is split (at least 8 blocks per split) until the grid covers the chip twice.
         const int64_t rt = cdiv(n, kTileRows);
         c.split_k = 1;
         c.waves = 8;
         int64_t wgs;
-        if ((wgs = cdiv(rt, 16) * cdiv(m, 128)) >= kCUs) {
+        if ((wgs = cdiv(rt, 8) * cdiv(m, 256)) >= kCUs) {
+            c.tile_m = 256;
+            c.tile_n = 128;
+        } else if ((wgs = cdiv(rt, 16) * cdiv(m, 128)) >= kCUs) {
             c.tile_m = 128;
             c.tile_n = 256;
         } else if ((wgs = cdiv(rt, 8) * cdiv(m, 64)) >= kCUs) {
@@ -1297,10 +1301,13 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
                       cfg->kernel == MAMBO_GEMM_TILED,
                   MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
     if (cfg->kernel == MAMBO_GEMM_TILED) {
-        MAMBO_REQUIRE(cfg->tile_m == 64 || cfg->tile_m == 128, MAMBO_ERR_VALUE, "tiled: tile_m must be 64 or 128");
+        MAMBO_REQUIRE(cfg->tile_m == 64 || cfg->tile_m == 128 || cfg->tile_m == 256, MAMBO_ERR_VALUE,
+                      "tiled: tile_m must be 64, 128 or 256");
         MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE, "tiled: waves must be 4 or 8");
         MAMBO_REQUIRE(cfg->tile_n == 16 * cfg->waves || cfg->tile_n == 32 * cfg->waves, MAMBO_ERR_VALUE,
                       "tiled: tile_n must be 16 or 32 weight rows per wave");
+        MAMBO_REQUIRE(cfg->tile_m != 256 || (cfg->waves == 8 && cfg->tile_n == 128), MAMBO_ERR_VALUE,
+                      "tiled: tile_m=256 is built for 8 waves of 16 weight rows (tile_n=128)");
         MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                       "split_k must be in [1, K/256]");
         return MAMBO_OK;

@@ -262,13 +262,14 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
                         if waves * rows <= 256:
                             space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows})
     if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup x K split
-        for tile_m in (64, 128):
-            for waves in (4, 8):
-                for rows_per_wave in (16, 32):
-                    for split in (1, 2, 4):
-                        if split <= blocks:
-                            space.append({"kernel": _native.GEMM_TILED, "waves": waves, "split_k": split,
-                                          "tile_m": tile_m, "tile_n": rows_per_wave * waves})
+        shapes = [(tile_m, waves, rows) for tile_m in (64, 128) for waves in (4, 8) for rows in (16, 32)]
+        if m >= 128:
+            shapes.append((256, 8, 16))
+        for tile_m, waves, rows_per_wave in shapes:
+            for split in (1, 2, 4):
+                if split <= blocks:
+                    space.append({"kernel": _native.GEMM_TILED, "waves": waves, "split_k": split,
+                                  "tile_m": tile_m, "tile_n": rows_per_wave * waves})
     return space
 
 

@@ -90,6 +90,17 @@ def test_gemm_config_defaults_and_validation():
     split = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 4, "tile_m": 128,
                                           "tile_n": 128})
     assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(split)) == 0
+    # 256 tokens: built for 8 waves of 16 weight rows only
+    for fields, rc in (({"waves": 8, "tile_n": 128}, 0), ({"waves": 4, "tile_n": 64}, _native.MAMBO_ERR_VALUE),
+                       ({"waves": 8, "tile_n": 256}, _native.MAMBO_ERR_VALUE)):
+        c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "split_k": 1, "tile_m": 256, **fields})
+        assert lib.mambo_gemm_check_config(2048, 4096, 16, ctypes.byref(c)) == rc, fields
+    # prefill default: 256 x 128 x 8 when that still gives every CU a workgroup, else 128 x 256 x 8
+    for m, n, tile in ((2048, 4096, (256, 128)), (8192, 14336, (256, 128)), (512, 8192, (64, 128)),
+                       (512, 57344, (256, 128)), (256, 8192, (64, 128))):
+        c = _native.GemmConfig()
+        assert lib.mambo_gemm_default_config(m, n, 32, ctypes.byref(c)) == 0
+        assert (c.kernel, c.tile_m, c.tile_n, c.waves) == (_native.GEMM_TILED, *tile, 8), (m, n, c.as_dict())
     # moderate M on a long K: the tiled default splits K to fill the chip
     c = _native.GemmConfig()
     assert lib.mambo_gemm_default_config(64, 8192, 112, ctypes.byref(c)) == 0
