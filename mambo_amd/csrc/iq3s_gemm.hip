@@ -808,19 +808,53 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
 // ============================================================================ tiled kernel
 // Large M (prefill). A workgroup of W waves computes a 16*MT (tokens) x 16*NT*W (weight
 // rows) output tile over all of K. Per 256-weight block the activations of the tile's
-// tokens (16*MT rows x 256 bytes + 8 E8M0 scales each) are staged in LDS, double
-// buffered, with a 272-byte row pitch so the 16 rows read by one lane group start in
-// different LDS banks. Each wave decodes its NT weight tiles once per block into dense
-// hi/lo operands (as the dense kernel does) and reuses them for all MT token sub-tiles:
-// MT*NT*4 MFMAs per block and wave, the fp16 d applied per block in f32. The grid's x
-// runs over weight-row tiles (grouped projections start on a workgroup boundary), y
-// over token tiles.
+// tokens (16*MT rows x 256 bytes + 8 E8M0 scales each) are copied from global memory
+// straight into LDS (global_load_lds: no staging registers, no LDS store instructions),
+// double buffered in two static arrays; within a row, 16-byte chunk c sits at slot
+// c ^ (row & 15), so the 16 rows that one lane group reads fall in 16 different bank
+// groups. Each wave decodes its NT weight tiles once per block into dense hi/lo operands
+// (as the dense kernel does) and reuses them for all MT token sub-tiles: MT*NT*4 MFMAs
+// per block and wave, the fp16 d applied per block in f32. The grid's x runs over
+// weight-row tiles (grouped projections start on a workgroup boundary), y over token
+// tiles, z over K splits.
 
-constexpr int kTiledPitch = 272;
+// LDS image of one staged block: values [16*MT][256] (chunk-swizzled), scales [16*MT][8].
+template <int MT>
+struct TiledBlock {
+    static constexpr int kRows = 16 * MT;
+    static constexpr int kValues = kRows * 256;
+    static constexpr int kBytes = kValues + kRows * 8;
+};
 
-__host__ __device__ constexpr int tiled_lds_bytes(int MT)
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// Issue the copies of block b's activations into `buf` (buffer loads straight to LDS over
+// resources at the tile's first token row): one 1 KiB copy (4 rows, 16 bytes per lane)
+// per values instruction and one 256-byte copy (32 rows of scales, 4 bytes per lane) per
+// scale instruction, spread over the waves. Rows past M read row M-1 (their outputs are
+// never stored). Completion is awaited by the next workgroup barrier.
+template <int MT, int W>
+__device__ __forceinline__ void stage_block(uint8_t *buf, __amdgpu_buffer_rsrc_t xrows, uint32_t ldxv,
+                                            __amdgpu_buffer_rsrc_t srows, uint32_t ldxs, int last_row, int b, int wave,
+                                            int lane)
 {
-    return 2 * (16 * MT * kTiledPitch + 16 * MT * 8);
+    constexpr int kRows = TiledBlock<MT>::kRows;
+    constexpr int kVInst = kRows / 4;
+    static_assert(kVInst % W == 0, "values copies must spread evenly over the waves");
+#pragma unroll
+    for (int j = 0; j < kVInst / W; ++j) {
+        const int i = wave + j * W;
+        const int row = 4 * i + (lane >> 4);
+        const uint32_t c = (uint32_t)((lane & 15) ^ (row & 15));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrows, (lds_ptr)(buf + 1024 * i), 16,
+                                                 (uint32_t)min(row, last_row) * ldxv + 16u * c, 256u * b, 0, 0);
+    }
+    constexpr int kSInst = kRows / 32;
+    for (int i = wave; i < kSInst; i += W) {
+        const int row = 32 * i + (lane >> 1);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(srows, (lds_ptr)(buf + TiledBlock<MT>::kValues + 256 * i), 4,
+                                                 (uint32_t)min(row, last_row) * ldxs + 4u * (lane & 1), 8u * b, 0, 0);
+    }
 }
 
 // Decoded dense operands of NT weight tiles for one block (see the dense kernel).
@@ -842,12 +876,190 @@ __device__ __forceinline__ void decode_tiles(const WTile (&w)[NT], const uint8_t
     }
 }
 
+// MT x NT sub-tiles of one block: A fragments from the staged block (ao: this lane's byte
+// offsets of its two 16-byte pieces per K half inside a 16-row sub-tile, soff: its scale
+// offset), one chain of four MFMAs (K halves x hi/lo) per sub-tile, then the block's d in
+// f32. The fence per sub-tile keeps the compiler from hoisting every LDS read of the
+// block into registers.
+template <int MT, int NT>
+__device__ __forceinline__ void mfma_block(const uint8_t *buf, const uint32_t (&ao)[2][2], uint32_t soff,
+                                           const v8i (&bh)[NT][2], const v8i (&bl)[NT][2], const float (&d)[NT],
+                                           float (&acc)[MT][NT][4])
+{
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t *ar = buf + 4096 * mt;
+        const uint8_t *sr = buf + TiledBlock<MT>::kValues + 128 * mt + soff;
+        v8i av[2];
+        int sc[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 lo = *reinterpret_cast<const uint4 *>(ar + ao[h][0]);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(ar + ao[h][1]);
+            av[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            sc[h] = sr[h];
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bh[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bl[nt][0], c, 0, 0, 0, sc[0], 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bh[nt][1], c, 0, 0, 0, sc[1], 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bl[nt][1], c, 0, 0, 0, sc[1], 0, 128);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mt][nt][r] = __builtin_fmaf(c[r], d[nt], acc[mt][nt][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int MT, int NT, int W>
+__global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+                                                            const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
+                                                            GroupArgs ga, int B, int bps, int atomic)
+{
+    constexpr int kRows = TiledBlock<MT>::kRows;
+    constexpr int kThreads = W * 64;
+    __shared__ __align__(16) uint8_t s_buf0[TiledBlock<MT>::kBytes];
+    __shared__ __align__(16) uint8_t s_buf1[TiledBlock<MT>::kBytes];
+    __shared__ uint32_t s_lvl[512];
+    __shared__ uint4 s_split[16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, q = lane >> 4;
+
+    // this workgroup's projection; tile_begin counts workgroups here
+    const uint8_t *packed = ga.packed[0];
+    float *out = ga.out[0];
+    int64_t N = ga.n[0], ldo = ga.ldo[0], wg = blockIdx.x;
+#pragma unroll
+    for (int g = 1; g < kMaxGroup; ++g)
+        if (g < ga.count && (int64_t)blockIdx.x >= ga.tile_begin[g]) {
+            packed = ga.packed[g];
+            out = ga.out[g];
+            N = ga.n[g];
+            ldo = ga.ldo[g];
+            wg = blockIdx.x - ga.tile_begin[g];
+        }
+    const int64_t tiles = (N + kTileRows - 1) / kTileRows;
+    const int64_t m0 = (int64_t)blockIdx.y * kRows;
+    // weight tiles of this wave (clamped to the last tile; stores are masked)
+    __amdgpu_buffer_rsrc_t wt[NT];
+    int64_t tile[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        tile[nt] = wg * (NT * W) + wave * NT + nt;
+        wt[nt] = byte_rsrc(packed + min(tile[nt], tiles - 1) * (int64_t)B * kTileBytes);
+    }
+
+    for (int i = tid; i < 512; i += kThreads)
+        s_lvl[i] = c_grid.level[i];
+    if (tid < 16)
+        s_split[tid] = uint4{c_split.w[tid][0], c_split.w[tid][1], c_split.w[tid][2], c_split.w[tid][3]};
+
+    const __amdgpu_buffer_rsrc_t xrows = byte_rsrc(xv + m0 * ldxv), srows = byte_rsrc(xs + m0 * ldxs);
+    const int last_row = (int)min<int64_t>(M - 1 - m0, kRows - 1);
+    // A operand of lane (token row col of a sub-tile, q): per K half h the 16-byte chunks
+    // c = 8*(q>>1) + (q&1) + 2h and c + 4 of the row (see the dense kernel for the byte and
+    // scale order), at their swizzled slots; scale byte 4*(q&1) + 2*(q>>1) + h.
+    uint32_t ao[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+            ao[h][p] = 256u * col + 16u * ((8u * (q >> 1) + (q & 1) + 2u * h + 4u * p) ^ (uint32_t)col);
+    const uint32_t soff = 8u * col + 4u * (q & 1) + 2u * (q >> 1);
+
+    float acc[MT][NT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mt][nt][r] = 0.0f;
+
+    // K range of this workgroup: blocks [b0, b1) (grid z splits K; partial sums are
+    // added into an output zeroed beforehand)
+    const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
+    const int b0 = blockIdx.z * bps, b1 = min(B, b0 + bps);
+    WTile wcur[NT], wnext[NT];
+    v8i bh[NT][2], bl[NT][2];
+    float d[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+        wcur[nt] = load_w_rsrc(wt[nt], (uint32_t)b0 * kTileBytes, lane, col);
+    stage_block<MT, W>(s_buf0, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, b0, wave, lane);
+    __syncthreads();
+
+    // Block b: copy block b+1's activations into the other buffer and request its weight
+    // tiles, then decode block b's weights and run its MFMAs; the barrier at the end waits
+    // for the copies (and frees this buffer for block b+2's). Two fixed buffers (the loop
+    // is unrolled by two), so the compiler can tell the copy target from the buffer read.
+#define MAMBO_TILED_BLOCK(cur, nxt)                                                                                \
+    do {                                                                                                           \
+        stage_block<MT, W>(nxt, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, min(b + 1, b1 - 1), wave,    \
+                           lane);                                                                                  \
+        for (int nt = 0; nt < NT; ++nt)                                                                            \
+            wnext[nt] = load_w_rsrc(wt[nt], (uint32_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);                 \
+        __builtin_amdgcn_sched_barrier(0);                                                                         \
+        decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);                                                           \
+        mfma_block<MT, NT>(cur, ao, soff, bh, bl, d, acc);                                                         \
+        for (int nt = 0; nt < NT; ++nt)                                                                            \
+            wcur[nt] = wnext[nt];                                                                                  \
+        __syncthreads();                                                                                           \
+    } while (0)
+    for (int b = b0; b < b1; ++b) {
+        MAMBO_TILED_BLOCK(s_buf0, s_buf1);
+        if (++b == b1)
+            break;
+        MAMBO_TILED_BLOCK(s_buf1, s_buf0);
+    }
+#undef MAMBO_TILED_BLOCK
+
+    // D[i][j] of sub-tile (mt, nt): lane j + 16*(i/4), register i%4 -> token
+    // m0 + 16*mt + 4q + r, weight row 16*tile + col.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int64_t n = tile[nt] * kTileRows + col;
+        if (n >= N)
+            continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + 16 * mt + 4 * q + r;
+                if (m < M) {
+                    if (atomic)
+                        atomicAdd(out + m * ldo + n, acc[mt][nt][r]);
+                    else
+                        out[m * ldo + n] = acc[mt][nt][r];
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------- register-staged form
+// The 256-token tile (MT=16): its two 68 KiB buffers leave no room for a third, so the
+// block copied into LDS must be one requested a block earlier; this form loads block b+2
+// into registers during block b and stores it at the top of block b+1 instead (two
+// blocks of latency cover), into double-buffered dynamic LDS with a 272-byte row pitch
+// (the 16 rows read by one lane group start in different banks). Measured 3-9% faster
+// than the direct copy for this tile, and slower than it for the smaller ones.
+constexpr int kTiledPitch = 272;
+
+__host__ __device__ constexpr int tiled_lds_bytes(int MT)
+{
+    return 2 * (16 * MT * kTiledPitch + 16 * MT * 8);
+}
+
 // MT x NT sub-tiles of one block: A fragments from the staged block (a: values at this
 // lane's row/column offset, sa: scales), one chain of four MFMAs (K halves x hi/lo) per
 // sub-tile, then the block's d in f32. The fence per sub-tile keeps the compiler from
 // hoisting every LDS read of the block into registers.
 template <int MT, int NT>
-__device__ __forceinline__ void mfma_block(const uint8_t *a, const uint8_t *sa, const v8i (&bh)[NT][2],
+__device__ __forceinline__ void mfma_block_pitched(const uint8_t *a, const uint8_t *sa, const v8i (&bh)[NT][2],
                                            const v8i (&bl)[NT][2], const float (&d)[NT], float (&acc)[MT][NT][4])
 {
 #pragma unroll
@@ -879,7 +1091,7 @@ __device__ __forceinline__ void mfma_block(const uint8_t *a, const uint8_t *sa, 
 }
 
 template <int MT, int NT, int W>
-__global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+__global__ __launch_bounds__(W * 64) void gemm_tiled_regs_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
 {
@@ -1003,7 +1215,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
             wnext[nt] = load_w_rsrc(wt[nt], (uint32_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);
         __builtin_amdgcn_sched_barrier(0);
         decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);
-        mfma_block<MT, NT>(smem + (b & 1) * kABytes + aoff, smem + 2 * kABytes + (b & 1) * kSBytes + soff, bh, bl, d,
+        mfma_block_pitched<MT, NT>(smem + (b & 1) * kABytes + aoff, smem + 2 * kABytes + (b & 1) * kSBytes + soff, bh, bl, d,
                            acc);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
@@ -1136,8 +1348,12 @@ template <int MT, int NT, int W>
 void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
                     int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
-    hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv, ldxv, xs,
-                       ldxs, M, ga, B, bps, atomic);
+    if constexpr (MT >= 16)
+        hipLaunchKernelGGL((gemm_tiled_regs_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv,
+                           ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    else
+        hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs, ldxs, M, ga,
+                           B, bps, atomic);
 }
 
 // Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves).
@@ -1395,9 +1611,9 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);
         MAMBO_REQUIRE((uintptr_t)xs % 8 == 0 && ldxs % 8 == 0, MAMBO_ERR_VALUE,
                       "tiled: x_scales base and row stride must be 8-byte aligned");
-        // the staging loads address a token tile with 32-bit offsets
-        MAMBO_REQUIRE((int64_t)c.tile_m * ldxv < ((int64_t)1 << 32), MAMBO_ERR_VALUE,
-                      "tiled: activation row stride too large for tile_m=%d", c.tile_m);
+        // the staging copies address a token tile with 32-bit offsets
+        MAMBO_REQUIRE((int64_t)c.tile_m * ldxv < ((int64_t)1 << 32) && (int64_t)c.tile_m * ldxs < ((int64_t)1 << 32),
+                      MAMBO_ERR_VALUE, "tiled: activation row stride too large for tile_m=%d", c.tile_m);
         // workgroups per projection; tile_begin counts workgroups for this kernel
         GroupArgs gt = ga;
         int64_t wgs = 0;
