@@ -564,8 +564,9 @@ __device__ __forceinline__ void to_dense_order(v8i &b)
     }
 }
 
-__device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, const uint8_t *lvl,
-                                              const uint4 *split, float (&acc)[4], bool valid)
+template <int MC>
+__device__ __forceinline__ void compute_dense(const WTile &w, const ADense (&at)[MC], const uint8_t *lvl,
+                                              const uint4 *split, float (&acc)[MC][4], bool valid)
 {
     const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
     const uint32_t sc = w.sc;
@@ -578,40 +579,61 @@ __device__ __forceinline__ void compute_dense(const WTile &w, const ADense &at, 
     to_dense_order(l0);
     to_dense_order(h1);
     to_dense_order(l1);
-    // B scale 2^1: the split terms are stored halved.
-    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    // one chain of four MFMAs: the callers interleave the chains of their NT tiles
-    v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], h0, zero, 0, 0, 0, (int)at.s[0], 0, 128);
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[0], l0, c, 0, 0, 0, (int)at.s[0], 0, 128);
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], h1, c, 0, 0, 0, (int)at.s[1], 0, 128);
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[1], l1, c, 0, 0, 0, (int)at.s[1], 0, 128);
+    // B scale 2^1: the split terms are stored halved. Per 16-token chunk one chain of four
+    // MFMAs on the one decode (the callers interleave the chains of their NT tiles).
     const float f = valid ? half_bits_to_float((uint16_t)w.dh) : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        acc[r] = __builtin_fmaf(c[r], f, acc[r]);
+    for (int u = 0; u < MC; ++u) {
+        const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[0], h0, zero, 0, 0, 0, (int)at[u].s[0], 0, 128);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[0], l0, c, 0, 0, 0, (int)at[u].s[0], 0, 128);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[1], h1, c, 0, 0, 0, (int)at[u].s[1], 0, 128);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[1], l1, c, 0, 0, 0, (int)at[u].s[1], 0, 128);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[u][r] = __builtin_fmaf(c[r], f, acc[u][r]);
+    }
+}
+
+// Activation fragments of all MC token chunks for block b (from the LDS copy when
+// kLdsAct, else from global memory through the resources xr, sr).
+template <bool kLdsAct, int MC>
+__device__ __forceinline__ void load_acts_dense(ADense (&a)[MC], const uint8_t *xbase, const uint8_t *sbase,
+                                                __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t sr,
+                                                const uint32_t (&xoff)[MC], const uint32_t (&soff)[MC], int b)
+{
+#pragma unroll
+    for (int u = 0; u < MC; ++u) {
+        if constexpr (kLdsAct)
+            load_a_dense(a[u], xbase, xoff[u], sbase, soff[u], b);
+        else
+            load_a_dense_rsrc(a[u], xr, xoff[u], sr, soff[u], b);
+    }
 }
 
 // Dynamic LDS of the dense kernel (level grid and split tables sit in static LDS):
-// cross-wave partial sums [W][NT][4][64] f32 and - when kLdsAct - the chunk's activation
-// rows [rows][K] and scales [rows][K/32].
+// cross-wave partial sums [W][NT][MC][4][64] f32 and - when kLdsAct - the workgroup's
+// activation rows [rows][K] and scales [rows][K/32].
 struct DenseLds {
     int red, x, xs, total;
 };
 
-__host__ __device__ inline DenseLds dense_lds(int W, int NT, int rows, int K, bool lds_act)
+__host__ __device__ inline DenseLds dense_lds(int W, int NT, int MC, int rows, int K, bool lds_act)
 {
     DenseLds l;
     l.red = 0;
-    l.x = l.red + (W > 1 ? W * NT * 4 * 64 * 4 : 0);
+    l.x = l.red + (W > 1 ? W * NT * MC * 4 * 64 * 4 : 0);
     l.xs = l.x + (lds_act ? rows * K : 0);
     l.total = l.xs + (lds_act ? rows * (K / 32) : 0);
     return l;
 }
 
-// A workgroup covers NT weight tiles (16*NT rows); each wave applies one activation
-// fragment per block to all NT tiles, so activation loads per weight byte drop by NT.
-// Grouped projections start on a workgroup boundary (tile_begin counts workgroups).
-template <int W, int NT, bool kLdsAct>
+// A workgroup covers NT weight tiles (16*NT rows) and MC chunks of 16 tokens; each wave
+// applies one activation fragment per block and chunk to all NT tiles (activation loads
+// per weight byte drop by NT) and each decoded tile-block to all MC chunks (decode work
+// per token drops by MC). Grouped projections start on a workgroup boundary
+// (tile_begin counts workgroups).
+template <int W, int NT, bool kLdsAct, int MC>
 __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
@@ -622,9 +644,9 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = B * 256;
-    const int64_t m0 = (int64_t)blockIdx.z * 16;
-    const int rows = (int)min<int64_t>(16, M - m0);
-    const DenseLds L = dense_lds(W, NT, rows, K, kLdsAct);
+    const int64_t m0 = (int64_t)blockIdx.z * (16 * MC);
+    const int rows = (int)min<int64_t>(16 * MC, M - m0);
+    const DenseLds L = dense_lds(W, NT, MC, rows, K, kLdsAct);
     const uint8_t *packed = ga.packed[0];
     float *out = ga.out[0];
     int64_t N = ga.n[0], ldo = ga.ldo[0], wg = blockIdx.x;
@@ -671,28 +693,34 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     __syncthreads();
     const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
 
-    // A lane: token col of the chunk, bytes of group 4*(q>>1) + h, half q&1 (+64 bytes for
-    // group 4*(q>>1) + 2 + h), scale of group 4*(q&1) + 2*(q>>1) + h. Lanes of tokens past
-    // M read the chunk's last token: they only feed output rows that are never stored.
-    const int rowc = min(col, rows - 1);
+    // A lane of chunk u: token 16u + col, bytes of group 4*(q>>1) + h, half q&1 (+64 bytes
+    // for group 4*(q>>1) + 2 + h), scale of group 4*(q&1) + 2*(q>>1) + h. Lanes of tokens
+    // past M read the last token: they only feed output rows that are never stored.
     const uint32_t xo = 32u * (4 * (q >> 1)) + 16u * (q & 1), so = 4u * (q & 1) + 2u * (q >> 1);
     const uint8_t *xbase = smem + L.x, *sbase = smem + L.xs;     // kLdsAct
     __amdgpu_buffer_rsrc_t xr = byte_rsrc(xv + m0 * ldxv), sr = byte_rsrc(xs + m0 * ldxs); // otherwise
-    uint32_t xoff, soff;
-    if constexpr (kLdsAct) {
-        xoff = (uint32_t)(rowc * K) + xo;
-        soff = (uint32_t)(rowc * (K / 32)) + so;
-    } else {
-        xoff = (uint32_t)(rowc * ldxv) + xo;
-        soff = (uint32_t)(rowc * ldxs) + so;
+    uint32_t xoff[MC], soff[MC];
+#pragma unroll
+    for (int u = 0; u < MC; ++u) {
+        const int rowc = min(16 * u + col, rows - 1);
+        if constexpr (kLdsAct) {
+            xoff[u] = (uint32_t)(rowc * K) + xo;
+            soff[u] = (uint32_t)(rowc * (K / 32)) + so;
+        } else {
+            xoff[u] = (uint32_t)(rowc * ldxv) + xo;
+            soff[u] = (uint32_t)(rowc * ldxs) + so;
+        }
     }
 
-    float acc[NT][4];
+    float acc[NT][MC][4];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            acc[nt][r] = 0.0f;
+        for (int u = 0; u < MC; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[nt][u][r] = 0.0f;
+#define load_acts(a, b) load_acts_dense<kLdsAct, MC>(a, xbase, sbase, xr, sr, xoff, soff, b)
     if (count > 0) {
         if constexpr (NT >= 4) {
             // Per tile: decode step i's block, then reload the same registers with step
@@ -702,26 +730,26 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
             // the registers of a two-step ring (occupancy 3 instead of 2, measured faster);
             // with fewer tiles the distance gets too short and the two-step ring is used.
             WTile wr[NT];
-            ADense ar[kLdsAct ? 1 : 2];
+            ADense ar[kLdsAct ? 1 : 2][MC];
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
                 wr[nt] = load_w_rsrc(wt[nt], (uint32_t)first * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
-                load_a_dense_rsrc(ar[0], xr, xoff, sr, soff, first);
+                load_acts(ar[0], first);
             for (int i0 = 0; i0 < count; i0 += 2) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int i = i0 + j;
                     const int bn = min(first + (i + 1) * W, last);
                     if constexpr (!kLdsAct)
-                        load_a_dense_rsrc(ar[j ^ 1], xr, xoff, sr, soff, bn);
+                        load_acts(ar[j ^ 1], bn);
                     else
-                        load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
+                        load_acts(ar[0], min(first + i * W, last));
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt) {
                         if constexpr (MAMBO_SCHED_FENCE)
                             __builtin_amdgcn_sched_barrier(0);
-                        compute_dense(wr[nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
+                        compute_dense<MC>(wr[nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
                         wr[nt] = load_w_rsrc(wt[nt], (uint32_t)bn * kTileBytes, lane, col);
                     }
                     if constexpr (MAMBO_SCHED_FENCE)
@@ -731,14 +759,14 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         } else {
             // Two-step ring: step i+1's blocks and activations load while step i decodes.
             WTile wr[kDepth][NT];
-            ADense ar[kLdsAct ? 1 : kDepth];
+            ADense ar[kLdsAct ? 1 : kDepth][MC];
 #pragma unroll
             for (int j = 0; j < kDepth - 1; ++j) {
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
                     wr[j][nt] = load_w_rsrc(wt[nt], (uint32_t)min(first + j * W, last) * kTileBytes, lane, col);
                 if constexpr (!kLdsAct)
-                    load_a_dense_rsrc(ar[j], xr, xoff, sr, soff, min(first + j * W, last));
+                    load_acts(ar[j], min(first + j * W, last));
             }
             for (int i0 = 0; i0 < count; i0 += kDepth) {
 #pragma unroll
@@ -750,14 +778,14 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                     for (int nt = 0; nt < NT; ++nt)
                         wr[slot][nt] = load_w_rsrc(wt[nt], (uint32_t)bp * kTileBytes, lane, col);
                     if constexpr (!kLdsAct)
-                        load_a_dense_rsrc(ar[slot], xr, xoff, sr, soff, bp);
+                        load_acts(ar[slot], bp);
                     if constexpr (MAMBO_SCHED_FENCE)
                         __builtin_amdgcn_sched_barrier(0);
                     if constexpr (kLdsAct)
-                        load_a_dense(ar[0], xbase, xoff, sbase, soff, min(first + i * W, last));
+                        load_acts(ar[0], min(first + i * W, last));
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt)
-                        compute_dense(wr[j][nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
+                        compute_dense<MC>(wr[j][nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
                     if constexpr (MAMBO_SCHED_FENCE)
                         __builtin_amdgcn_sched_barrier(0);
                 }
@@ -765,43 +793,51 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
         }
     }
 
-    // D[i][j] of the MFMA sits in lane j + 16*(i/4), register i%4: token 4q + r, weight
-    // row col. The waves hold partial sums over disjoint K blocks.
+#undef load_acts
+
+    // D[i][j] of the MFMA sits in lane j + 16*(i/4), register i%4: token 16u + 4q + r,
+    // weight row col. The waves hold partial sums over disjoint K blocks.
     if constexpr (W > 1) {
         float *red = reinterpret_cast<float *>(smem + L.red);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                red[((wave * NT + nt) * 4 + r) * 64 + lane] = acc[nt][r];
+            for (int u = 0; u < MC; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    red[(((wave * NT + nt) * MC + u) * 4 + r) * 64 + lane] = acc[nt][u][r];
         __syncthreads();
         if (wave != 0)
             return;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = 0.0f;
+            for (int u = 0; u < MC; ++u)
 #pragma unroll
-                for (int w = 0; w < W; ++w)
-                    v += red[((w * NT + nt) * 4 + r) * 64 + lane];
-                acc[nt][r] = v;
-            }
+                for (int r = 0; r < 4; ++r) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < W; ++w)
+                        v += red[(((w * NT + nt) * MC + u) * 4 + r) * 64 + lane];
+                    acc[nt][u][r] = v;
+                }
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int64_t n = (wg * NT + nt) * kTileRows + col;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + 4 * q + r;
-            if (m < M && n < N) {
-                float *o = out + m * ldo + n;
-                if (atomic)
-                    atomicAdd(o, acc[nt][r]);
-                else
-                    *o = acc[nt][r];
+        for (int u = 0; u < MC; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + 16 * u + 4 * q + r;
+                if (m < M && n < N) {
+                    float *o = out + m * ldo + n;
+                    if (atomic)
+                        atomicAdd(o, acc[nt][u][r]);
+                    else
+                        *o = acc[nt][u][r];
+                }
             }
-        }
     }
 }
 
@@ -1302,44 +1338,57 @@ int launch_stream_u(int waves, bool lds_act, const StreamLaunch &sl, hipStream_t
     return MAMBO_OK;
 }
 
-template <int W, int NT>
-void launch_dense_wn(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                     const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+template <int W, int NT, int MC>
+void launch_dense_wnm(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+                      const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     if (lds_act)
-        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, true>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
-                           ga, B, bps, atomic);
+        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, true, MC>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs,
+                           M, ga, B, bps, atomic);
     else
-        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, false>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs, M,
-                           ga, B, bps, atomic);
+        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, false, MC>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs,
+                           M, ga, B, bps, atomic);
 }
 
 template <int NT>
-int launch_dense_n(int waves, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
+int launch_dense_n(int waves, int mc, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
                    int atomic)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_dense_wn<WV, NT>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);             \
+        launch_dense_wnm<WV, NT, 1>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);         \
         break;
+#define MAMBO_W2(WV)                                                                                               \
+    case WV:                                                                                                       \
+        launch_dense_wnm<WV, NT, 2>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);         \
+        break;
+    if (mc == 2) {
+        switch (waves) {
+            MAMBO_W2(2) MAMBO_W2(4) MAMBO_W2(8)
+        default:
+            return mambo_fail(MAMBO_ERR_VALUE, "dense kernel with tile_m=32: waves must be 2, 4 or 8 (got %d)", waves);
+        }
+        return MAMBO_OK;
+    }
     switch (waves) {
         MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
     default:
         return mambo_fail(MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16 (got %d)", waves);
     }
 #undef MAMBO_W
+#undef MAMBO_W2
     return MAMBO_OK;
 }
 
-int launch_dense(int waves, int nt, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
+int launch_dense(int waves, int nt, int mc, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
                  int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
                  int atomic)
 {
     switch (nt) {
-    case 1: return launch_dense_n<1>(waves, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
-    case 2: return launch_dense_n<2>(waves, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
-    case 4: return launch_dense_n<4>(waves, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 1: return launch_dense_n<1>(waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 2: return launch_dense_n<2>(waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 4: return launch_dense_n<4>(waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
     default: return mambo_fail(MAMBO_ERR_VALUE, "dense kernel: tile_n must be 16, 32 or 64 (got %d)", 16 * nt);
     }
 }
@@ -1468,19 +1517,24 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
     if (m <= 4 && units * 16 <= kTargetWaves / 4 && blocks % 16 == 0 && blocks / 16 >= 2)
         waves = 16;
     if (c.kernel == MAMBO_GEMM_DENSE) {
-        // Dense: 4 waves, and as many weight tiles per workgroup (sharing each activation
-        // fragment) as still leave a workgroup per CU; measured on gfx950 at M = 8..16.
-        const int64_t rt = cdiv(n, kTileRows);
-        int nt = 1;
-        for (int t : {2, 4})
-            if (cdiv(rt, t) * cdiv(m, 16) >= kCUs)
-                nt = t;
-        c.tile_n = kTileRows * nt;
+        // Dense: 4 waves; above 16 tokens, 32 tokens per workgroup (each decoded tile-block
+        // serves two 16-token chunks); and as many weight tiles per workgroup (sharing each
+        // activation fragment) as still leave a workgroup per CU at 16 tokens, or 5/8 of
+        // one at 32 (measured on gfx950: M = 8..16, and M = 24..48 on the 70B shapes).
         waves = 1;
         for (int w : {2, 4})
             if (blocks % w == 0 && blocks / w >= 2)
                 waves = w;
-        units = cdiv(rt, nt) * cdiv(m, 16);
+        const int mc = m > 16 && waves >= 2 ? 2 : 1;
+        c.tile_m = 16 * mc;
+        const int64_t rt = cdiv(n, kTileRows), mchunks = cdiv(m, 16 * mc);
+        const int64_t min_wgs = mc == 2 ? kCUs * 5 / 8 : kCUs;
+        int nt = 1;
+        for (int t : {2, 4})
+            if (cdiv(rt, t) * mchunks >= min_wgs)
+                nt = t;
+        c.tile_n = kTileRows * nt;
+        units = cdiv(rt, nt) * mchunks;
     }
     if (c.kernel == MAMBO_GEMM_STREAM) {
         // Runs of tiles per workgroup: about two workgroups per CU (512) walking their
@@ -1529,10 +1583,14 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
         return MAMBO_OK;
     }
     MAMBO_REQUIRE(valid_waves(cfg->waves), MAMBO_ERR_VALUE, "waves must be one of 1, 2, 4, 6, 8, 12, 16");
-    if (cfg->kernel == MAMBO_GEMM_DENSE)
+    if (cfg->kernel == MAMBO_GEMM_DENSE) {
         MAMBO_REQUIRE(cfg->tile_n == 0 || cfg->tile_n == 16 || cfg->tile_n == 32 || cfg->tile_n == 64,
                       MAMBO_ERR_VALUE, "dense: tile_n must be 16, 32 or 64 weight rows");
-    else
+        MAMBO_REQUIRE(cfg->tile_m == 0 || cfg->tile_m == 16 || cfg->tile_m == 32, MAMBO_ERR_VALUE,
+                      "dense: tile_m must be 16 or 32 tokens");
+        MAMBO_REQUIRE(cfg->tile_m != 32 || cfg->waves == 2 || cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE,
+                      "dense: tile_m=32 is built for 2, 4 or 8 waves");
+    } else
         MAMBO_REQUIRE(cfg->tile_n >= 0 && cfg->tile_n % kTileRows == 0 && cfg->tile_n <= (1 << 20), MAMBO_ERR_VALUE,
                       "stream: tile_n must be a multiple of 16 weight rows, at most 2^20");
     MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
@@ -1639,6 +1697,8 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     const int B = (int)blocks;
     if (c.kernel == MAMBO_GEMM_DENSE) {
         const int nt = c.tile_n ? c.tile_n / kTileRows : 1;
+        const int mc = c.tile_m == 32 ? 2 : 1; // 16-token chunks per workgroup
+        const int drows = (int)std::min<int64_t>(16 * mc, m);
         // workgroups per projection (NT tiles each); tile_begin counts workgroups
         GroupArgs gd = ga;
         int64_t wgs = 0;
@@ -1647,10 +1707,15 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
             wgs += cdiv(cdiv(ga.n[g], kTileRows), nt);
         }
         grid.x = (unsigned)wgs;
-        if (lds_act && dense_lds(c.waves, nt, rows, (int)k, true).total > kMaxDynLds)
+        grid.z = (unsigned)cdiv(m, 16 * mc);
+        lds_act = (int64_t)drows * k * 33 / 32 <= kMaxLdsAct;
+        if (lds_act && dense_lds(c.waves, nt, mc, drows, (int)k, true).total > kMaxDynLds)
             lds_act = false;
-        const DenseLds L = dense_lds(c.waves, nt, rows, (int)k, lds_act);
-        rc = launch_dense(c.waves, nt, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, gd, B, bps, atomic);
+        const DenseLds L = dense_lds(c.waves, nt, mc, drows, (int)k, lds_act);
+        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
+                      "configuration needs %d bytes of LDS per workgroup (waves=%d, tile_n=%d, tile_m=%d)", L.total,
+                      c.waves, c.tile_n, c.tile_m);
+        rc = launch_dense(c.waves, nt, mc, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, gd, B, bps, atomic);
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
         if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > kMaxDynLds)

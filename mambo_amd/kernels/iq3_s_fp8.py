@@ -242,8 +242,8 @@ def launch_iq3_s_fp8_matmul_grouped(x_values: torch.Tensor, x_scales: torch.Tens
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
     search spaces of iq3_s_fp8.py:416-459): stream kernels (block-diagonal or dense
-    activations) x waves per workgroup x K split x weight rows per workgroup, and for
-    M >= 32 the tiled kernel's tile shapes."""
+    activations) x waves per workgroup x K split x weight rows (and, dense above 16
+    tokens, tokens) per workgroup, and for M >= 32 the tiled kernel's tile shapes."""
     blocks = k // IQ3_S_BLOCK_VALUES
     u = min(4, -(-m // 4))
     space = []
@@ -257,10 +257,12 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
                 if kernel == _native.GEMM_STREAM:  # runs of 1..8 tiles per workgroup
                     for rows in ((16, 32, 64, 128) if split == 1 else (16,)):
                         space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows})
-                else:  # weight tiles per workgroup sharing one activation fragment
+                else:  # weight tiles per workgroup sharing one activation fragment, tokens per workgroup
                     for rows in (16, 32, 64):
-                        if waves * rows <= 256:
-                            space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows})
+                        for tokens in ((16, 32) if m > 16 and waves in (2, 4, 8) else (16,)):
+                            if waves * rows * tokens // 16 <= 256:
+                                space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows,
+                                              "tile_m": tokens})
     if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup x K split
         shapes = [(tile_m, waves, rows) for tile_m in (64, 128) for waves in (4, 8) for rows in (16, 32)]
         if m >= 128:

@@ -95,6 +95,16 @@ def test_gemm_config_defaults_and_validation():
                        ({"waves": 8, "tile_n": 256}, _native.MAMBO_ERR_VALUE)):
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "split_k": 1, "tile_m": 256, **fields})
         assert lib.mambo_gemm_check_config(2048, 4096, 16, ctypes.byref(c)) == rc, fields
+    # dense default: 32 tokens per workgroup above 16 tokens; tiles per workgroup by grid size
+    for m, n, tile_m, tile_n in ((16, 8192, 16, 32), (16, 57344, 16, 64), (32, 57344, 32, 64), (32, 8192, 32, 32),
+                                 (32, 10240, 32, 64), (24, 8192, 32, 32), (48, 57344, 32, 64)):
+        c = _native.GemmConfig()
+        assert lib.mambo_gemm_default_config(m, n, 32, ctypes.byref(c)) == 0
+        assert (c.kernel, c.tile_m, c.tile_n, c.waves) == (_native.GEMM_DENSE, tile_m, tile_n, 4), (m, n, c.as_dict())
+    for fields, rc in (({"tile_m": 32, "waves": 4}, 0), ({"tile_m": 32, "waves": 16}, _native.MAMBO_ERR_VALUE),
+                       ({"tile_m": 48, "waves": 4}, _native.MAMBO_ERR_VALUE)):
+        c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_DENSE, "split_k": 1, **fields})
+        assert lib.mambo_gemm_check_config(32, 4096, 16, ctypes.byref(c)) == rc, fields
     # prefill default: 256 x 128 x 8 when that still gives every CU a workgroup, else 128 x 256 x 8
     for m, n, tile in ((2048, 4096, (256, 128)), (8192, 14336, (256, 128)), (512, 8192, (64, 128)),
                        (512, 57344, (256, 128)), (256, 8192, (64, 128))):
