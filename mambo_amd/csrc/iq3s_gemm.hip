@@ -1480,7 +1480,10 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         c.split_k = 1;
         c.waves = 8;
         int64_t wgs;
-        if ((wgs = cdiv(rt, 8) * cdiv(m, 256)) >= kCUs) {
+        // (the 256-token tile only where its token padding is within 1/8 of the 128-token
+        // tile's: never for M < 256)
+        const bool fits256 = m >= 256 && cdiv(m, 256) * 256 * 8 <= cdiv(m, 128) * 128 * 9;
+        if (fits256 && (wgs = cdiv(rt, 8) * cdiv(m, 256)) >= kCUs) {
             c.tile_m = 256;
             c.tile_n = 128;
         } else if ((wgs = cdiv(rt, 16) * cdiv(m, 128)) >= kCUs) {

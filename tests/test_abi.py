@@ -107,7 +107,8 @@ def test_gemm_config_defaults_and_validation():
         assert lib.mambo_gemm_check_config(32, 4096, 16, ctypes.byref(c)) == rc, fields
     # prefill default: 256 x 128 x 8 when that still gives every CU a workgroup, else 128 x 256 x 8
     for m, n, tile in ((2048, 4096, (256, 128)), (8192, 14336, (256, 128)), (512, 8192, (64, 128)),
-                       (512, 57344, (256, 128)), (256, 8192, (64, 128))):
+                       (512, 57344, (256, 128)), (256, 8192, (64, 128)), (64, 57344, (64, 128)),
+                       (128, 57344, (64, 128)), (384, 57344, (128, 256))):
         c = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(m, n, 32, ctypes.byref(c)) == 0
         assert (c.kernel, c.tile_m, c.tile_n, c.waves) == (_native.GEMM_TILED, *tile, 8), (m, n, c.as_dict())
