@@ -1283,12 +1283,24 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_regs_kernel(const uint8_t *
 #undef MAMBO_STORE_STAGE
 }
 
-__global__ void zero_rows_kernel(float *__restrict__ out, int64_t rows, int64_t cols, int64_t ld)
+// Zero row blockIdx.y of projection blockIdx.z's output (the split-K accumulators of
+// every projection of a launch in one dispatch). The projection is picked by selects
+// over constant indices, so the arguments stay in scalar registers.
+__global__ void zero_rows_kernel(GroupArgs ga)
 {
+    const int g = blockIdx.z;
+    float *out = ga.out[0];
+    int64_t cols = ga.n[0], ld = ga.ldo[0];
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+        if (g == i) {
+            out = ga.out[i];
+            cols = ga.n[i];
+            ld = ga.ldo[i];
+        }
     const int64_t r = blockIdx.y;
     for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += (int64_t)gridDim.x * blockDim.x)
         out[r * ld + c] = 0.0f;
-    (void)rows;
 }
 
 // Launch arguments of the stream kernel beyond the operands.
@@ -1471,32 +1483,33 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
                : m < kTiledMinM          ? MAMBO_GEMM_DENSE
                                          : MAMBO_GEMM_TILED;
     if (c.kernel == MAMBO_GEMM_TILED) {
-        // The largest tile that still gives every CU a workgroup (measured on gfx950:
-        // 256 tokens x 128 weight rows x 8 waves is fastest when the grid fills the chip,
-        // 4-8% ahead of 128 x 256 x 8 - each decoded weight tile serves 16 token sub-tiles;
-        // then 64 x 128 x 8 and 64 x 64 x 4); when even the smallest leaves CUs idle, K
-        // is split (at least 8 blocks per split) until the grid covers the chip twice.
+        // 128 tokens x 128 weight rows x 8 waves when that gives every CU a workgroup
+        // (measured on gfx950 over the 8B and 70B projections at 512-8192 tokens: the
+        // fastest tile or within 3% of it, ahead of 256 x 128 x 8 by up to 16% where that
+        // grid ends in a partial round), then 64 x 128 x 8; when even that leaves CUs idle,
+        // K is split (at least 8 blocks per split) until the grid covers the chip twice.
+        // On long K (at least 48 blocks: the down projections) the 128-token tile stays
+        // and K is split (at least 16 blocks per split) until the grid covers the chip
+        // twice (measured: 8192 x 28672 at 256 and 512 tokens, 4096 x 14336 at 512,
+        // 20-30% faster than 64 x 128 tiles).
         const int64_t rt = cdiv(n, kTileRows);
         c.split_k = 1;
         c.waves = 8;
+        c.tile_n = 128;
         int64_t wgs;
-        // (the 256-token tile only where its token padding is within 1/8 of the 128-token
-        // tile's: never for M < 256)
-        const bool fits256 = m >= 256 && cdiv(m, 256) * 256 * 8 <= cdiv(m, 128) * 128 * 9;
-        if (fits256 && (wgs = cdiv(rt, 8) * cdiv(m, 256)) >= kCUs) {
-            c.tile_m = 256;
-            c.tile_n = 128;
-        } else if ((wgs = cdiv(rt, 16) * cdiv(m, 128)) >= kCUs) {
+        // (the 128-token tile only where its token padding is within 1/8 of the 64-token
+        // tile's: never for M < 128)
+        const bool fits128 = m >= 128 && cdiv(m, 128) * 128 * 8 <= cdiv(m, 64) * 64 * 9;
+        const bool long_k = blocks >= 48;
+        if (fits128 && ((wgs = cdiv(rt, 8) * cdiv(m, 128)) >= kCUs || long_k)) {
             c.tile_m = 128;
-            c.tile_n = 256;
-        } else if ((wgs = cdiv(rt, 8) * cdiv(m, 64)) >= kCUs) {
-            c.tile_m = 64;
-            c.tile_n = 128;
+            if (long_k && wgs < 2 * kCUs)
+                c.split_k = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv(2 * kCUs, wgs), blocks / 16));
         } else {
             c.tile_m = 64;
-            c.tile_n = 128;
             wgs = cdiv(rt, 8) * cdiv(m, 64);
-            c.split_k = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv(2 * kCUs, wgs), blocks / 8));
+            if (wgs < kCUs)
+                c.split_k = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv(2 * kCUs, wgs), blocks / 8));
         }
         // Few weight rows (k/v projections) leave even the split grid small: up to 255
         // tokens the dense kernel's 16-token chunks are faster there (measured).
@@ -1660,13 +1673,14 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     const int atomic = splits > 1;
     if (atomic) {
         MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
-        for (int g = 0; g < count; ++g) {
-            dim3 zg((unsigned)std::min<int64_t>(cdiv(ga.n[g], 256), 1024), (unsigned)m);
-            hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, ga.out[g], m, ga.n[g], ga.ldo[g]);
-            rc = mambo_check_launch("zero_rows");
-            if (rc)
-                return rc;
-        }
+        int64_t n_max = 0;
+        for (int g = 0; g < count; ++g)
+            n_max = std::max(n_max, ga.n[g]);
+        dim3 zg((unsigned)std::min<int64_t>(cdiv(n_max, 256), 1024), (unsigned)m, (unsigned)count);
+        hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, ga);
+        rc = mambo_check_launch("zero_rows");
+        if (rc)
+            return rc;
     }
     if (c.kernel == MAMBO_GEMM_TILED) {
         const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);

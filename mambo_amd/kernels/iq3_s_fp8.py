@@ -145,6 +145,11 @@ def select_config(m: int, n: int, k: int, arch: str | None = None) -> dict:
     tuned = _tuned_table().get(arch, {}).get(tuned_key(n, k, m))
     if tuned is not None:
         return dict(tuned)
+    return default_config(m, arch)
+
+
+def default_config(m: int, arch: str = "gfx950") -> dict:
+    """The configuration used for M tokens when the tuned table has no entry."""
     return dict(BEST_CONFIGS[arch]["medium" if m < LARGE_TOKEN_THRESHOLD else "large"])
 
 
@@ -241,13 +246,16 @@ def launch_iq3_s_fp8_matmul_grouped(x_values: torch.Tensor, x_scales: torch.Tens
 
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
-    search spaces of iq3_s_fp8.py:416-459): stream kernels (block-diagonal or dense
-    activations) x waves per workgroup x K split x weight rows (and, dense above 16
-    tokens, tokens) per workgroup, and for M >= 32 the tiled kernel's tile shapes."""
+    search spaces of iq3_s_fp8.py:416-459), led by the library default for the token
+    count: the block-diagonal stream kernel up to 16 tokens and the dense kernel up to
+    128 (each re-reads every weight once per 16- or 32-token chunk, so neither is a
+    candidate beyond), x waves per workgroup x K split x weight rows (and, dense above 16
+    tokens, tokens) per workgroup; for M >= 32 the tiled kernel's tile shapes."""
     blocks = k // IQ3_S_BLOCK_VALUES
     u = min(4, -(-m // 4))
-    space = []
-    for kernel in (_native.GEMM_STREAM, _native.GEMM_DENSE):
+    space = [default_config(m)]
+    families = [kern for kern, limit in ((_native.GEMM_STREAM, 16), (_native.GEMM_DENSE, 128)) if m <= limit]
+    for kernel in families:
         for waves in (1, 2, 4, 6, 8, 12, 16):
             if waves > blocks or (kernel == _native.GEMM_STREAM and waves * u > 32):
                 continue
@@ -275,15 +283,23 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     return space
 
 
-def make_benchmark_cases(iq3_weight: torch.Tensor, tokens: tuple[int, ...] = (4, 128)) -> list:
+def make_benchmark_cases(iq3_weight: torch.Tensor, tokens: tuple[int, ...] = (4, 128), *,
+                         rotate_bytes: int = 0, max_copies: int = 64) -> list:
     """Prepare weights and MXFP8 inputs once; benchmark only the projection
-    (iq3_s_fp8.py:402-465). ``iq3_weight`` is raw GGUF uint8 [N,B,110] on the GPU."""
+    (iq3_s_fp8.py:402-465). ``iq3_weight`` is raw GGUF uint8 [N,B,110] on the GPU.
+    With ``rotate_bytes`` the cases cycle over copies of the packed weight (together at
+    least that many bytes, at most ``max_copies``), so that each launch streams its
+    weight from HBM as the projections of a many-layer decode step do."""
+    from dataclasses import replace
+
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
     from mambo_amd.utils.kernel_benchmark import BenchmarkCase
 
-    fields = prepare_iq3_s_fields(iq3_weight)
+    fields = prepare_iq3_s_fields(iq3_weight, fields=False)
     n_rows, k_blocks = _weight_dimensions(fields)
     k = k_blocks * IQ3_S_BLOCK_VALUES
+    copies = max(1, min(max_copies, -(-int(rotate_bytes) // fields.packed.numel())))
+    weights = [fields] + [replace(fields, packed=fields.packed.clone()) for _ in range(copies - 1)]
     stream = torch.cuda.current_stream()
     gen = torch.Generator(device=iq3_weight.device)
     gen.manual_seed(0)
@@ -292,13 +308,17 @@ def make_benchmark_cases(iq3_weight: torch.Tensor, tokens: tuple[int, ...] = (4,
         x = torch.randn((m, k), dtype=torch.float32, device=iq3_weight.device, generator=gen)
         x_values, x_scales = launch_quantize_fp8(x, stream=stream)
         out = torch.empty((m, n_rows), dtype=torch.float32, device=iq3_weight.device)
+        turn = [0]
 
         def launch(config):
-            launch_iq3_s_fp8_matmul(x_values, x_scales, fields, stream=stream, config=config, out=out)
+            # the current stream: the capture stream while a timing graph is recorded
+            w = weights[turn[0] % copies]
+            turn[0] += 1
+            launch_iq3_s_fp8_matmul(x_values, x_scales, w, config=config, out=out)
 
         return BenchmarkCase(name=f"M={m} N={n_rows} K={k}", stream=stream, launch=launch,
                              search_space=gemm_search_space(m, n_rows, k),
                              summary_keys=("kernel", "waves", "split_k", "tile_m", "tile_n"),
-                             key=tuned_key(n_rows, k, m))
+                             key=tuned_key(n_rows, k, m), rotation=copies, default=default_config(m))
 
     return [make_case(m) for m in tokens]

@@ -5,6 +5,13 @@ benchmark cases; this module searches each case's launch configurations, re-time
 winner with the reference's three timers (mean_us with a sync per launch, batched_us,
 event_us; 5 warm-up and 20 iterations, kernel_benchmark.py:56-94) and reports it.
 
+Candidates are timed as the projections run in a decode step: each case rotates over
+enough copies of its weight that every launch streams the weight from HBM (the
+reference re-launches on one weight, which the 256 MB memory-side cache then holds for
+the smaller projections), and the launches are replayed from a captured HIP graph, so
+that a 5 us kernel is not timed as the host's launch rate. The library default is one
+of the candidates; a tuned entry replaces it only when it is faster by ``min_gain``.
+
     python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --model M.gguf --weight-name NAME
     python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --synthetic 4096 4096 [--write-table]
 
@@ -18,6 +25,7 @@ from __future__ import annotations
 import argparse
 import importlib
 import json
+import math
 from dataclasses import dataclass, field
 from pathlib import Path
 from time import perf_counter
@@ -41,6 +49,10 @@ class BenchmarkCase:
     # Per-invocation state reset, included in reported timings after tuning.
     before_launch_fn: Callable[[Config], None] | None = None
     key: str = ""
+    # launches per timed graph: `launch` cycles over this many weight copies
+    rotation: int = 1
+    # the library's own configuration for the shape (a member of search_space), if any
+    default: Config | None = None
 
 
 @dataclass
@@ -54,6 +66,29 @@ class TuneResult:
     tuner_us: float
     successes: list = field(default_factory=list)
     failures: list = field(default_factory=list)
+    default_us: float | None = None  # the library default's time (None: not a candidate)
+    default_of: Config | None = None
+
+    @property
+    def is_default(self) -> bool:
+        """The library default won (or no candidate beat it by the required margin)."""
+        return self.default_us is not None and self.best == self.default_of
+
+
+def _graph_time(stream, fn, launches: int, target_us: float = 2000.0, max_reps: int = 20) -> float:
+    """Average time of `fn` over `launches` calls captured in one HIP graph, replayed
+    until about `target_us` has been timed."""
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(launches):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    one = _time_events(stream, graph.replay, 1)
+    reps = max(1, min(max_reps, math.ceil(target_us / max(one, 1e-3))))
+    us = _time_events(stream, graph.replay, reps) / launches
+    del graph
+    return us
 
 
 def _time_events(stream, fn, iters: int) -> float:
@@ -67,20 +102,28 @@ def _time_events(stream, fn, iters: int) -> float:
     return start.elapsed_time(stop) * 1000.0 / iters
 
 
-def exhaustive_search(case: BenchmarkCase, *, warmup: int = 2, iters: int = 10):
-    """Time every configuration of the case; failures (invalid configs) are recorded."""
+def _time_config(case: BenchmarkCase, config: Config, *, warmup: int, iters: int, graph: bool) -> float:
+    def once() -> None:
+        if case.before_launch_fn is not None:
+            case.before_launch_fn(config)
+        case.launch(config)
+    for _ in range(max(warmup, 1)):
+        once()
+    torch.cuda.synchronize()
+    if graph:
+        return _graph_time(case.stream, once, max(case.rotation, 1))
+    return _time_events(case.stream, once, iters)
+
+
+def exhaustive_search(case: BenchmarkCase, *, warmup: int = 2, iters: int = 10, graph: bool = True):
+    """Time every configuration of the case; failures (invalid configs) are recorded.
+    Warm-up launches run eagerly (an invalid configuration raises there, before any
+    capture); with `graph` the timed launches are `case.rotation` launches replayed
+    from a HIP graph, else `iters` eager launches."""
     successes, failures = [], []
     for config in case.search_space:
-        def once(config=config):
-            if case.before_launch_fn is not None:
-                case.before_launch_fn(config)
-            case.launch(config)
         try:
-            for _ in range(warmup):
-                once()
-            torch.cuda.synchronize()
-            us = _time_events(case.stream, once, iters)
-            successes.append((config, us))
+            successes.append((config, _time_config(case, config, warmup=warmup, iters=iters, graph=graph)))
         except (ValueError, RuntimeError) as exc:
             failures.append((config, str(exc)))
     if not successes:
@@ -88,12 +131,31 @@ def exhaustive_search(case: BenchmarkCase, *, warmup: int = 2, iters: int = 10):
     return successes, failures
 
 
-def mini_benchmark(cases: Sequence[BenchmarkCase], *, quiet: bool = False) -> list[TuneResult]:
-    """Tune each case, then time the winner with any per-launch reset (kernel_benchmark.py:41-100)."""
+def _versus_default(case: BenchmarkCase, best: Config, *, graph: bool, rounds: int = 2) -> tuple[float, float]:
+    """Best-of-`rounds` times of the library default and `best`, timed alternately, so
+    that neither is favoured by its place in the search (clock ramp, cache state)."""
+    d_us, b_us = float("inf"), float("inf")
+    for _ in range(rounds):
+        d_us = min(d_us, _time_config(case, case.default, warmup=2, iters=10, graph=graph))
+        b_us = min(b_us, _time_config(case, best, warmup=2, iters=10, graph=graph))
+    return d_us, b_us
+
+
+def mini_benchmark(cases: Sequence[BenchmarkCase], *, quiet: bool = False, graph: bool = True,
+                   min_gain: float = 0.03) -> list[TuneResult]:
+    """Tune each case, then time the winner with any per-launch reset (kernel_benchmark.py:41-100).
+    The case's library default stays the answer unless the search's winner, re-timed
+    alternately with it, is at least `min_gain` (a fraction) faster."""
     results = []
     for case in cases:
-        successes, failures = exhaustive_search(case)
+        successes, failures = exhaustive_search(case, graph=graph)
         best, tuner_us = min(successes, key=lambda item: item[1])
+        default_us = next((us for config, us in successes if config == case.default), None)
+        if default_us is not None:
+            if best != case.default:
+                default_us, tuner_us = _versus_default(case, best, graph=graph)
+            if tuner_us > default_us * (1.0 - min_gain):
+                best, tuner_us = case.default, default_us
 
         def launch_once() -> None:
             if case.before_launch_fn is not None:
@@ -120,28 +182,37 @@ def mini_benchmark(cases: Sequence[BenchmarkCase], *, quiet: bool = False) -> li
         batched_us = measure(batched=True)
         event_us = _time_events(case.stream, launch_once, 20)
         result = TuneResult(case.name, case.key, dict(best), mean_us, batched_us, event_us, tuner_us,
-                            successes, failures)
+                            successes, failures, default_us,
+                            dict(case.default) if case.default is not None else None)
         results.append(result)
         if not quiet:
+            versus = "" if default_us is None else (
+                " (library default)" if result.is_default else f" (library default {default_us:.3f})")
             print(f"{case.name}: best_config={best}, "
                   f"mean_us={mean_us:.3f}, batched_us={batched_us:.3f}, "
                   f"event_us={event_us:.3f}, "
-                  f"tuner_us={tuner_us:.3f} (warmup=5, iterations=20), "
-                  f"candidates={len(successes)} passed/{len(failures)} failed")
+                  f"tuner_us={tuner_us:.3f}{versus} (warmup=5, iterations=20), "
+                  f"candidates={len(successes)} passed/{len(failures)} failed", flush=True)
             if case.summary_keys:
                 by_group: dict[tuple[Any, ...], float] = {}
                 for config, us in successes:
-                    group = tuple(config[key] for key in case.summary_keys)
+                    group = tuple(config.get(key, 0) for key in case.summary_keys)
                     by_group[group] = min(by_group.get(group, float("inf")), us)
                 print(f"  best latency by {case.summary_keys} (us): {by_group}")
     return results
 
 
 def write_tuned_table(results: Sequence[TuneResult], path: Path, arch: str) -> None:
+    """Merge the winners into the table; a shape whose library default won loses any
+    entry it had."""
     table = json.loads(path.read_text()) if path.exists() else {}
     entries = table.setdefault(arch, {})
     for r in results:
-        if r.key:
+        if not r.key:
+            continue
+        if r.is_default:
+            entries.pop(r.key, None)
+        else:
             entries[r.key] = r.best
     path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
 
@@ -188,24 +259,35 @@ def benchmark_main(argv: Sequence[str] | None = None) -> list[TuneResult]:
     parser.add_argument("kernel", choices=sorted(_BENCHMARKS))
     parser.add_argument("--model", type=Path, help="GGUF model path")
     parser.add_argument("--weight-name", help="tensor name in the GGUF model")
-    parser.add_argument("--synthetic", nargs=2, type=int, metavar=("N", "K"),
-                        help="use a random IQ3_S weight of this shape instead of a GGUF tensor")
+    parser.add_argument("--synthetic", nargs=2, type=int, metavar=("N", "K"), action="append",
+                        help="use a random IQ3_S weight of this shape instead of a GGUF tensor (repeatable)")
     parser.add_argument("--tokens", type=int, nargs="+", default=[4, 128], help="token counts M to tune")
     parser.add_argument("--write-table", action="store_true", help="store winners in the tuned table")
+    parser.add_argument("--table", type=Path, help="tuned table to write (default: the one the launcher reads)")
+    parser.add_argument("--rotate-mib", type=int, default=512,
+                        help="weight copies per case to at least this many MiB (at most 64 copies)")
+    parser.add_argument("--min-gain", type=float, default=0.03,
+                        help="fraction by which a candidate must beat the library default")
+    parser.add_argument("--no-graph", action="store_true", help="time candidates by eager launches")
     args = parser.parse_args(argv)
 
     expected_type, kernel_module, factory = _BENCHMARKS[args.kernel]
     if args.synthetic:
-        weight = synthetic_weight(*args.synthetic)
+        sources = [lambda shape=shape: synthetic_weight(*shape) for shape in args.synthetic]
     elif args.model and args.weight_name:
-        weight = load_gguf_weight(args.model, args.weight_name, expected_type)
+        sources = [lambda: load_gguf_weight(args.model, args.weight_name, expected_type)]
     else:
         parser.error("give --model and --weight-name, or --synthetic N K")
     module = importlib.import_module(kernel_module)
-    results = mini_benchmark(getattr(module, factory)(weight, tuple(args.tokens)))
+    results = []
+    for source in sources:
+        cases = getattr(module, factory)(source(), tuple(args.tokens), rotate_bytes=args.rotate_mib << 20)
+        results += mini_benchmark(cases, graph=not args.no_graph, min_gain=args.min_gain)
+        del cases
+        torch.cuda.empty_cache()
     if args.write_table:
         from mambo_amd import _native
-        write_tuned_table(results, module.TUNED_PATH, _native.device_arch())
+        write_tuned_table(results, args.table or module.TUNED_PATH, _native.device_arch())
     return results
 
 

@@ -105,13 +105,20 @@ def test_gemm_config_defaults_and_validation():
                        ({"tile_m": 48, "waves": 4}, _native.MAMBO_ERR_VALUE)):
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_DENSE, "split_k": 1, **fields})
         assert lib.mambo_gemm_check_config(32, 4096, 16, ctypes.byref(c)) == rc, fields
-    # prefill default: 256 x 128 x 8 when that still gives every CU a workgroup, else 128 x 256 x 8
-    for m, n, tile in ((2048, 4096, (256, 128)), (8192, 14336, (256, 128)), (512, 8192, (64, 128)),
-                       (512, 57344, (256, 128)), (256, 8192, (64, 128)), (64, 57344, (64, 128)),
-                       (128, 57344, (64, 128)), (384, 57344, (128, 256))):
+    # prefill default: 128 x 128 x 8 when that still gives every CU a workgroup (and pads
+    # the tokens by at most 1/8 more than 64-token tiles), else 64 x 128 x 8; on long K
+    # (>= 48 blocks) the 128-token tile with K split until the grid covers the chip twice
+    for m, n, blocks, tile, split in ((2048, 4096, 32, (128, 128), 1), (8192, 14336, 32, (128, 128), 1),
+                                      (512, 8192, 32, (128, 128), 1), (512, 57344, 32, (128, 128), 1),
+                                      (256, 8192, 32, (64, 128), 1), (64, 57344, 32, (64, 128), 1),
+                                      (128, 57344, 32, (128, 128), 1), (384, 57344, 32, (128, 128), 1),
+                                      (192, 57344, 32, (64, 128), 1), (256, 8192, 112, (128, 128), 4),
+                                      (512, 8192, 112, (128, 128), 2), (2048, 8192, 112, (128, 128), 1),
+                                      (512, 4096, 56, (128, 128), 3), (128, 8192, 112, (128, 128), 7)):
         c = _native.GemmConfig()
-        assert lib.mambo_gemm_default_config(m, n, 32, ctypes.byref(c)) == 0
-        assert (c.kernel, c.tile_m, c.tile_n, c.waves) == (_native.GEMM_TILED, *tile, 8), (m, n, c.as_dict())
+        assert lib.mambo_gemm_default_config(m, n, blocks, ctypes.byref(c)) == 0
+        assert (c.kernel, c.tile_m, c.tile_n, c.waves, c.split_k) == (_native.GEMM_TILED, *tile, 8, split), \
+            (m, n, blocks, c.as_dict())
     # moderate M on a long K: the tiled default splits K to fill the chip
     c = _native.GemmConfig()
     assert lib.mambo_gemm_default_config(64, 8192, 112, ctypes.byref(c)) == 0

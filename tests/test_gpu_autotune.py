@@ -27,7 +27,8 @@ def test_autotune_search_winner_and_table(gpu, tmp_path, monkeypatch):
     n, k = 256, 2048
     step(f"synthetic weight {n}x{k}, tune M=4 and M=64")
     raw = synthetic_weight(n, k, seed=11)
-    cases = iq3_s_fp8.make_benchmark_cases(raw, tokens=(4, 64))
+    cases = iq3_s_fp8.make_benchmark_cases(raw, tokens=(4, 64), rotate_bytes=4 << 20)
+    assert all(c.rotation == -(-(4 << 20) // (n * k // 256 * 110)) for c in cases)
     results = mini_benchmark(cases, quiet=True)
     assert [r.key for r in results] == [iq3_s_fp8.tuned_key(n, k, 4), iq3_s_fp8.tuned_key(n, k, 64)]
     for case, r in zip(cases, results):
@@ -35,6 +36,9 @@ def test_autotune_search_winner_and_table(gpu, tmp_path, monkeypatch):
         assert not r.failures, r.failures[:3]
         assert len(r.successes) == len(case.search_space)
         assert r.event_us > 0 and r.mean_us > 0 and r.batched_us > 0
+        # the library default is timed, and only a 3% faster candidate replaces it
+        assert r.default_us is not None and r.default_of == case.default
+        assert r.is_default or r.tuner_us <= 0.97 * r.default_us
     # the winners reproduce the oracle
     fields = prepare_iq3_s_fields(raw)
     raw_np = raw.cpu().numpy()

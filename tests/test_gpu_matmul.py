@@ -272,15 +272,20 @@ def test_grouped_into_strided_outputs(gpu):
     raws = [make_synthetic_iq3_s(n, k, seed=60 + n) for n in (20, 33)]
     fields = [prepare_iq3_s_fields(torch.from_numpy(r).to(gpu)) for r in raws]
     xv, xs = oracle.quantize_mxfp8(np.random.default_rng(3).standard_normal((m, k)).astype(np.float32))
-    big = torch.full((m, 80), 7.0, dtype=torch.float32, device=gpu)
-    step("grouped matmul into column slices of one buffer")
-    launch_iq3_s_fp8_matmul_grouped(torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu), fields,
-                                    outs=[big[:, 4:24], big[:, 40:73]])
-    torch.cuda.synchronize()
-    b = big.cpu().numpy()
-    check(b[:, 4:24], oracle.iq3s_fp8_matmul(xv, xs, raws[0]))
-    check(b[:, 40:73], oracle.iq3s_fp8_matmul(xv, xs, raws[1]))
-    assert np.all(b[:, :4] == 7.0) and np.all(b[:, 24:40] == 7.0) and np.all(b[:, 73:] == 7.0)
+    from mambo_amd import _native
+    # the K-split form zeroes the slices first (one dispatch for all projections) and
+    # must leave the columns between them alone
+    for cfg in (None, {"kernel": _native.GEMM_STREAM, "waves": 2, "split_k": 2},
+                {"kernel": _native.GEMM_DENSE, "waves": 1, "split_k": 4}):
+        big = torch.full((m, 80), 7.0, dtype=torch.float32, device=gpu)
+        step(f"grouped matmul into column slices of one buffer, cfg={cfg}")
+        launch_iq3_s_fp8_matmul_grouped(torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu), fields,
+                                        outs=[big[:, 4:24], big[:, 40:73]], config=cfg)
+        torch.cuda.synchronize()
+        b = big.cpu().numpy()
+        check(b[:, 4:24], oracle.iq3s_fp8_matmul(xv, xs, raws[0]))
+        check(b[:, 40:73], oracle.iq3s_fp8_matmul(xv, xs, raws[1]))
+        assert np.all(b[:, :4] == 7.0) and np.all(b[:, 24:40] == 7.0) and np.all(b[:, 73:] == 7.0)
 
 
 @pytest.mark.parametrize("m", [64, 100, 128, 257])

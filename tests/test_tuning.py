@@ -105,3 +105,49 @@ def test_tuned_table_round_trip_and_lookup(tmp_path, monkeypatch):
         assert iq3_s_fp8.select_config(17, 4096, 4096, arch="gfx950") == iq3_s_fp8.BEST_CONFIGS["gfx950"]["medium"]
     finally:
         iq3_s_fp8._tuned_table.cache_clear()
+
+
+def test_search_space_families_and_validity():
+    """The library default leads every search space; stream candidates only up to 16
+    tokens, dense up to 128, tiled from 32; every candidate passes the library's own
+    configuration check for its shape (no launches)."""
+    import ctypes
+
+    from mambo_amd import _native
+    from mambo_amd.kernels import iq3_s_fp8
+    lib = _native.lib()
+    for m, n, k in ((1, 8192, 8192), (4, 57344, 8192), (16, 4096, 14336), (32, 8192, 8192), (64, 10240, 8192),
+                    (128, 4096, 4096), (512, 8192, 28672), (2048, 28672, 4096)):
+        space = iq3_s_fp8.gemm_search_space(m, n, k)
+        assert space[0] == iq3_s_fp8.default_config(m)
+        kernels = {c["kernel"] for c in space[1:]}
+        assert (_native.GEMM_STREAM in kernels) == (m <= 16), m
+        assert (_native.GEMM_DENSE in kernels) == (m <= 128), m
+        assert (_native.GEMM_TILED in kernels) == (m >= 32), m
+        assert len({tuple(sorted(c.items())) for c in space}) == len(space)
+        for c in space:
+            cfg = _native.GemmConfig.from_dict(c)
+            if c["kernel"] != _native.GEMM_AUTO:
+                assert lib.mambo_gemm_check_config(m, n, k // 256, ctypes.byref(cfg)) == 0, (m, n, k, c)
+
+
+def test_tuned_table_drops_shapes_the_default_won(tmp_path, monkeypatch):
+    from mambo_amd.kernels import iq3_s_fp8
+    from mambo_amd.utils.kernel_benchmark import TuneResult, write_tuned_table
+    path = tmp_path / "tuned.json"
+    key = iq3_s_fp8.tuned_key(8192, 8192, 4)
+    tuned = {"kernel": 1, "waves": 4, "split_k": 1, "tile_n": 32}
+    write_tuned_table([TuneResult("M=4", key, tuned, 1.0, 1.0, 1.0, 9.0, default_us=10.0,
+                                  default_of=iq3_s_fp8.default_config(4))], path, "gfx950")
+    monkeypatch.setattr(iq3_s_fp8, "TUNED_PATH", path)
+    iq3_s_fp8._tuned_table.cache_clear()
+    try:
+        assert iq3_s_fp8.select_config(4, 8192, 8192, arch="gfx950") == tuned
+        won = TuneResult("M=4", key, iq3_s_fp8.default_config(4), 1.0, 1.0, 1.0, 10.0, default_us=10.0,
+                         default_of=iq3_s_fp8.default_config(4))
+        assert won.is_default
+        write_tuned_table([won], path, "gfx950")
+        iq3_s_fp8._tuned_table.cache_clear()
+        assert iq3_s_fp8.select_config(4, 8192, 8192, arch="gfx950") == iq3_s_fp8.default_config(4)
+    finally:
+        iq3_s_fp8._tuned_table.cache_clear()
