@@ -81,7 +81,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_rsrc(const void *base)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)0xFFFFFFFFu, 0x00020000);
 }
 
-// load_w through a buffer resource: the tile at byte `step` past the resource base.
+// LDS destination of the direct global-to-LDS copies.
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// load_w through a buffer resource: the tile at byte `step` past the resource base
+// (kWLoads vector memory instructions).
+constexpr int kWLoads = 5;
 __device__ __forceinline__ WTile load_w_rsrc(__amdgpu_buffer_rsrc_t r, uint32_t step, uint32_t lane, uint32_t col)
 {
     WTile w;
@@ -359,9 +364,42 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     const int first = b_begin + wave;
     const int col = lane & 15, q = lane >> 4;
 
+    // Staging copies (codebook, activation rows and their scales) go from global memory
+    // straight into LDS ahead of the ring's first weight loads: vector memory counts
+    // complete in issue order, so the barrier below waits for the copies (L2) and not for
+    // the weights (HBM), which stay in flight across it.
+    __shared__ uint32_t s_grid[512];
+    const uint8_t *lut = reinterpret_cast<const uint8_t *>(s_grid);
+    {
+        const __amdgpu_buffer_rsrc_t gr = byte_rsrc(c_grid.fp8);
+        for (int i = wave; i < 8; i += W)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (lds_ptr)(s_grid + 64 * i), 4, 4u * lane, 256u * i, 0, 0);
+        if constexpr (kLdsAct) {
+            // activation rows m0 .. m0+rows-1 as 16-byte chunks (K is a multiple of 256, so
+            // none straddles rows), then their scales as dwords (K/32 is a multiple of 8;
+            // the host stages only 4-byte aligned scale rows)
+            const int nx = rows * K / 16;
+            const __amdgpu_buffer_rsrc_t xr = byte_rsrc(xv + m0 * ldxv);
+            for (int i = wave; 64 * i < nx; i += W) {
+                const int c = 64 * i + lane, r = c * 16 / K;
+                if (c < nx)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(smem + L.x + 1024 * i), 16,
+                                                             (uint32_t)(r * ldxv + (c * 16 - r * K)), 0, 0, 0);
+            }
+            const int ns = rows * (K / 128);
+            const __amdgpu_buffer_rsrc_t sr = byte_rsrc(xs + m0 * ldxs);
+            for (int i = wave; 64 * i < ns; i += W) {
+                const int e = 64 * i + lane, r = e / (K / 128);
+                if (e < ns)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_ptr)(smem + L.xs + 256 * i), 4,
+                                                             (uint32_t)(r * ldxs + 4 * (e - r * (K / 128))), 0, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     // Ring of kDepth register sets with fixed slots (the loop body is unrolled kDepth
-    // times): step s is decoded while steps s+1 .. s+kDepth-1 are in flight. The first
-    // loads go out before the activations are staged.
+    // times): step s is decoded while steps s+1 .. s+kDepth-1 are in flight.
     WTile wr[kDepth];
     StreamCursor pc = {0, 0, t_begin, byte_rsrc(tile_ref(ga, t_begin, B).w)};
 #pragma unroll
@@ -369,31 +407,14 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
         wr[j] = load_w_rsrc(pc.w, (uint32_t)min(first + pc.i * W, b_end - 1) * kTileBytes, lane, col);
         advance(pc, total, steps, ga, B);
     }
-
-    __shared__ uint32_t s_grid[512];
-    const uint8_t *lut = reinterpret_cast<const uint8_t *>(s_grid);
-    {
-        const int nt = W * 64;
-        for (int i = tid; i < 512; i += nt)
-            s_grid[i] = c_grid.fp8[i];
-        if (tid < 20)
-            reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 16 ? 0u : 0x7F7F7F7Fu;
-        if constexpr (kLdsAct) {
-            // activation rows m0 .. m0+rows-1: K is a multiple of 256, so 16-byte chunks
-            // never straddle rows
-            const int nx = rows * K / 16;
-            for (int c = tid; c < nx; c += nt) {
-                const int r = c * 16 / K;
-                *reinterpret_cast<uint4 *>(smem + L.x + c * 16) =
-                    *reinterpret_cast<const uint4 *>(xv + (m0 + r) * ldxv + (c * 16 - r * K));
-            }
-            const int ns = rows * (K / 32);
-            for (int i = tid; i < ns; i += nt) {
-                const int r = i / (K / 32);
-                smem[L.xs + i] = xs[(m0 + r) * ldxs + (i - r * (K / 32))];
-            }
-        }
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < 20)
+        reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 16 ? 0u : 0x7F7F7F7Fu;
+    // this wave's copies are done once at most the ring's kWLoads * (kDepth - 1) weight
+    // loads are outstanding (s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and
+    // lgkmcnt 11:8 left unconstrained)
+    static_assert(kWLoads * (kDepth - 1) < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt((kWLoads * (kDepth - 1)) | (7 << 4) | (15 << 8));
     __syncthreads();
 
     const bool a_lane = (col >> 2) == q;
@@ -670,27 +691,6 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
     const int first = b_begin + wave;
     const int count = first < b_end ? (b_end - first + W - 1) / W : 0;
     const int last = first + (count - 1) * W;
-    {
-        const int nthr = W * 64;
-        for (int i = tid; i < 512; i += nthr)
-            s_lvl[i] = c_grid.level[i];
-        if (tid < 16)
-            s_split[tid] = uint4{c_split.w[tid][0], c_split.w[tid][1], c_split.w[tid][2], c_split.w[tid][3]};
-        if constexpr (kLdsAct) {
-            const int nx = rows * K / 16;
-            for (int c = tid; c < nx; c += nthr) {
-                const int r = c * 16 / K;
-                *reinterpret_cast<uint4 *>(smem + L.x + c * 16) =
-                    *reinterpret_cast<const uint4 *>(xv + (m0 + r) * ldxv + (c * 16 - r * K));
-            }
-            const int ns = rows * (K / 32);
-            for (int i = tid; i < ns; i += nthr) {
-                const int r = i / (K / 32);
-                smem[L.xs + i] = xs[(m0 + r) * ldxs + (i - r * (K / 32))];
-            }
-        }
-    }
-    __syncthreads();
     const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
 
     // A lane of chunk u: token 16u + col, bytes of group 4*(q>>1) + h, half q&1 (+64 bytes
@@ -711,6 +711,71 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
             soff[u] = (uint32_t)(rowc * ldxs) + so;
         }
     }
+#define load_acts(a, b) load_acts_dense<kLdsAct, MC>(a, xbase, sbase, xr, sr, xoff, soff, b)
+
+    // Staging copies (level grid, split table and - when kLdsAct - the activation rows
+    // and scales) go from global memory straight into LDS ahead of the ring's first
+    // weight loads: vector memory counts complete in issue order, so the barrier waits
+    // for the copies (L2) and not for the weights (HBM), which stay in flight across it.
+    {
+        const __amdgpu_buffer_rsrc_t gr = byte_rsrc(c_grid.level), tr = byte_rsrc(&c_split.w[0][0]);
+        for (int i = wave; i < 9; i += W) {
+            if (i < 8)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (lds_ptr)(s_lvl + 64 * i), 4, 4u * lane, 256u * i, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(tr, (lds_ptr)s_split, 4, 4u * lane, 0, 0, 0);
+        }
+        if constexpr (kLdsAct) {
+            // rows as 16-byte chunks (K is a multiple of 256, so none straddles rows), then
+            // their scales as dwords (K/32 is a multiple of 8; the host stages only 4-byte
+            // aligned scale rows)
+            const int nx = rows * K / 16;
+            for (int i = wave; 64 * i < nx; i += W) {
+                const int c = 64 * i + lane, r = c * 16 / K;
+                if (c < nx)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(smem + L.x + 1024 * i), 16,
+                                                             (uint32_t)(r * ldxv + (c * 16 - r * K)), 0, 0, 0);
+            }
+            const int ns = rows * (K / 128);
+            for (int i = wave; 64 * i < ns; i += W) {
+                const int e = 64 * i + lane, r = e / (K / 128);
+                if (e < ns)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_ptr)(smem + L.xs + 256 * i), 4,
+                                                             (uint32_t)(r * ldxs + 4 * (e - r * (K / 128))), 0, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The ring's registers and its first loads. NT >= 4: per tile, decode step i's block,
+    // then reload the same registers with step i+1's block, so the next step's NT blocks
+    // are in flight during this step's decodes while only one block per tile is held (the
+    // activation fragments keep a ring of two). With four tiles that is a step of prefetch
+    // distance in half the registers of a two-step ring (occupancy 3 instead of 2,
+    // measured faster); with fewer tiles the distance gets too short and the two-step
+    // ring (step i+1's blocks and activations load while step i decodes) is used.
+    constexpr bool kReload = NT >= 4;
+    constexpr int kWSteps = kReload ? 1 : kDepth - 1; // steps loaded ahead of the loop
+    WTile wr[kReload ? 1 : kDepth][NT];
+    ADense ar[kLdsAct ? 1 : (kReload ? 2 : kDepth)][MC];
+    // (a wave without blocks loads block b_begin, unused, so every wave issues the same
+    // number of loads after its copies)
+#pragma unroll
+    for (int j = 0; j < kWSteps; ++j) {
+        const int blk = count > 0 ? min(first + j * W, last) : b_begin;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+            wr[j][nt] = load_w_rsrc(wt[nt], (uint32_t)blk * kTileBytes, lane, col);
+        if constexpr (!kLdsAct)
+            load_acts(ar[j], blk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's copies are done once at most its kWLoads * NT * kWSteps weight loads
+    // (issued after them) are outstanding
+    constexpr int kVm = kWLoads * NT * kWSteps;
+    static_assert(kVm < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt((kVm & 15) | (7 << 4) | (15 << 8) | ((kVm >> 4) << 14));
+    __syncthreads();
 
     float acc[NT][MC][4];
 #pragma unroll
@@ -720,22 +785,8 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 acc[nt][u][r] = 0.0f;
-#define load_acts(a, b) load_acts_dense<kLdsAct, MC>(a, xbase, sbase, xr, sr, xoff, soff, b)
     if (count > 0) {
-        if constexpr (NT >= 4) {
-            // Per tile: decode step i's block, then reload the same registers with step
-            // i+1's block, so the next step's NT blocks are in flight during this step's
-            // decodes while only one block per tile is held (the activation fragments keep
-            // a ring of two). With four tiles that is a step of prefetch distance in half
-            // the registers of a two-step ring (occupancy 3 instead of 2, measured faster);
-            // with fewer tiles the distance gets too short and the two-step ring is used.
-            WTile wr[NT];
-            ADense ar[kLdsAct ? 1 : 2][MC];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-                wr[nt] = load_w_rsrc(wt[nt], (uint32_t)first * kTileBytes, lane, col);
-            if constexpr (!kLdsAct)
-                load_acts(ar[0], first);
+        if constexpr (kReload) {
             for (int i0 = 0; i0 < count; i0 += 2) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
@@ -749,25 +800,14 @@ __global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__res
                     for (int nt = 0; nt < NT; ++nt) {
                         if constexpr (MAMBO_SCHED_FENCE)
                             __builtin_amdgcn_sched_barrier(0);
-                        compute_dense<MC>(wr[nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
-                        wr[nt] = load_w_rsrc(wt[nt], (uint32_t)bn * kTileBytes, lane, col);
+                        compute_dense<MC>(wr[0][nt], ar[kLdsAct ? 0 : j], lvl, s_split, acc[nt], i < count);
+                        wr[0][nt] = load_w_rsrc(wt[nt], (uint32_t)bn * kTileBytes, lane, col);
                     }
                     if constexpr (MAMBO_SCHED_FENCE)
                         __builtin_amdgcn_sched_barrier(0);
                 }
             }
         } else {
-            // Two-step ring: step i+1's blocks and activations load while step i decodes.
-            WTile wr[kDepth][NT];
-            ADense ar[kLdsAct ? 1 : kDepth][MC];
-#pragma unroll
-            for (int j = 0; j < kDepth - 1; ++j) {
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    wr[j][nt] = load_w_rsrc(wt[nt], (uint32_t)min(first + j * W, last) * kTileBytes, lane, col);
-                if constexpr (!kLdsAct)
-                    load_acts(ar[j], min(first + j * W, last));
-            }
             for (int i0 = 0; i0 < count; i0 += kDepth) {
 #pragma unroll
                 for (int j = 0; j < kDepth; ++j) {
@@ -862,7 +902,6 @@ struct TiledBlock {
     static constexpr int kBytes = kValues + kRows * 8;
 };
 
-typedef __attribute__((address_space(3))) void *lds_ptr;
 
 // Issue the copies of block b's activations into `buf` (buffer loads straight to LDS over
 // resources at the tile's first token row): one 1 KiB copy (4 rows, 16 bytes per lane)
@@ -1726,6 +1765,8 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         grid.x = (unsigned)wgs;
         grid.z = (unsigned)cdiv(m, 16 * mc);
         lds_act = (int64_t)drows * k * 33 / 32 <= kMaxLdsAct;
+        if ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0) // the staging copies move scales as dwords
+            lds_act = false;
         if (lds_act && dense_lds(c.waves, nt, mc, drows, (int)k, true).total > kMaxDynLds)
             lds_act = false;
         const DenseLds L = dense_lds(c.waves, nt, mc, drows, (int)k, lds_act);
@@ -1736,6 +1777,9 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
         if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > kMaxDynLds)
+            lds_act = false;
+        // the staging copies move activation scales as dwords
+        if ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0)
             lds_act = false;
         const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
         MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
