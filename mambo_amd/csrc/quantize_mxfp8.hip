@@ -20,22 +20,28 @@ namespace {
 // |x * 2^-e| <= 448.
 constexpr bool kQuantHwCvt = true;
 
+// The input is read once and the codes written once: both go through with the
+// non-temporal hint (bf16 [4096,4096] from a HIP graph: 3.89 -> 4.34 TB/s).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <bool kBf16>
 __device__ __forceinline__ void load8(const void *__restrict__ x, int64_t off, float v[8])
 {
     if constexpr (kBf16) {
-        uint4 r = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + off);
-        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+        const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(x) + off));
+        uint32_t w[4] = {r[0], r[1], r[2], r[3]};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             v[2 * i] = __uint_as_float(w[i] << 16);
             v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
         }
     } else {
-        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + off);
-        float4 a = p[0], b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        const f32x4 *p = reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(x) + off);
+        const f32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+        v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+        v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
     }
 }
 
@@ -104,7 +110,7 @@ __global__ __launch_bounds__(256) void quantize_mxfp8_kernel(const void *__restr
             out.y = pack4<kHw>(y[4], y[5], y[6], y[7]);
             uint8_t *vp = values + row * ldv + 32 * g + 8 * j;
             if constexpr (kVec) {
-                *reinterpret_cast<uint2 *>(vp) = out;
+                __builtin_nontemporal_store(u32x2{out.x, out.y}, reinterpret_cast<u32x2 *>(vp));
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
