@@ -1118,7 +1118,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
                     if (atomic)
                         atomicAdd(out + m * ldo + n, acc[mt][nt][r]);
                     else
-                        out[m * ldo + n] = acc[mt][nt][r];
+                        __builtin_nontemporal_store(acc[mt][nt][r], out + m * ldo + n); // written once
                 }
             }
     }
@@ -1323,7 +1323,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_regs_kernel(const uint8_t *
                     if (atomic)
                         atomicAdd(out + m * ldo + n, acc[mt][nt][r]);
                     else
-                        out[m * ldo + n] = acc[mt][nt][r];
+                        __builtin_nontemporal_store(acc[mt][nt][r], out + m * ldo + n); // written once
                 }
             }
     }
