@@ -998,7 +998,53 @@ __device__ __forceinline__ void mfma_block(const uint8_t *buf, const uint32_t (&
     }
 }
 
-template <int MT, int NT, int W>
+// Half-K form (the 256 x 256 x 16-wave tile, where the full-K form spills): per block,
+// decode K half 0 of the NT weight tiles, run its MFMAs for all MT sub-tiles, then half
+// 1; the decoded operands of one half and the block's weight registers (reloaded with
+// block b+1 right after their last decode) are all that is held, 128 VGPRs for 16
+// sub-tiles of accumulators. d is applied per half (acc += d*c0; acc += d*c1).
+template <int NT, int H>
+__device__ __forceinline__ void decode_half(const WTile (&w)[NT], const uint8_t *lvl, const uint4 *split,
+                                            v8i (&bh)[NT], v8i (&bl)[NT])
+{
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t s5[5] = {w[nt].ia.x, w[nt].ia.y, w[nt].ia.z, w[nt].ia.w, (uint32_t)w[nt].ib};
+        const uint4 t = split[H == 0 ? (w[nt].sc & 15u) : ((uint32_t)w[nt].sc >> 4)];
+        decode_split<H>(s5, H == 0 ? w[nt].sg.x : w[nt].sg.y, lvl, t, bh[nt], bl[nt],
+                        std::make_integer_sequence<int, 8>{});
+        to_dense_order(bh[nt]);
+        to_dense_order(bl[nt]);
+    }
+}
+
+template <int MT, int NT, int H>
+__device__ __forceinline__ void mfma_half(const uint8_t *buf, const uint32_t (&ao)[2][2], uint32_t soff,
+                                          const v8i (&bh)[NT], const v8i (&bl)[NT], const float (&d)[NT],
+                                          float (&acc)[MT][NT][4])
+{
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t *ar = buf + 4096 * mt;
+        const uint8_t *sr = buf + TiledBlock<MT>::kValues + 128 * mt + soff;
+        const uint4 lo = *reinterpret_cast<const uint4 *>(ar + ao[H][0]);
+        const uint4 hi = *reinterpret_cast<const uint4 *>(ar + ao[H][1]);
+        const v8i av = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        const int sc = sr[H];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bh[nt], zero, 0, 0, 0, sc, 0, 128);
+            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bl[nt], c, 0, 0, 0, sc, 0, 128);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mt][nt][r] = __builtin_fmaf(c[r], d[nt], acc[mt][nt][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int MT, int NT, int W, bool kHalf = false>
 __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
@@ -1068,8 +1114,9 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     // added into an output zeroed beforehand)
     const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
     const int b0 = blockIdx.z * bps, b1 = min(B, b0 + bps);
-    WTile wcur[NT], wnext[NT];
-    v8i bh[NT][2], bl[NT][2];
+    WTile wcur[NT], wnext[kHalf ? 1 : NT];
+    v8i bh[kHalf ? 1 : NT][2], bl[kHalf ? 1 : NT][2]; // full-K form
+    v8i hh[NT], hl[NT];                              // half-K form
     float d[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -1085,13 +1132,26 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     do {                                                                                                           \
         stage_block<MT, W>(nxt, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, min(b + 1, b1 - 1), wave,    \
                            lane);                                                                                  \
-        for (int nt = 0; nt < NT; ++nt)                                                                            \
-            wnext[nt] = load_w_rsrc<0>(wt[nt], (uint32_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);                 \
-        __builtin_amdgcn_sched_barrier(0);                                                                         \
-        decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);                                                           \
-        mfma_block<MT, NT>(cur, ao, soff, bh, bl, d, acc);                                                         \
-        for (int nt = 0; nt < NT; ++nt)                                                                            \
-            wcur[nt] = wnext[nt];                                                                                  \
+        const uint32_t next_ = (uint32_t)min(b + 1, b1 - 1) * kTileBytes;                                          \
+        if constexpr (kHalf) {                                                                                     \
+            __builtin_amdgcn_sched_barrier(0);                                                                     \
+            for (int nt = 0; nt < NT; ++nt)                                                                        \
+                d[nt] = half_bits_to_float((uint16_t)wcur[nt].dh);                                                 \
+            decode_half<NT, 0>(wcur, lvl, s_split, hh, hl);                                                        \
+            mfma_half<MT, NT, 0>(cur, ao, soff, hh, hl, d, acc);                                                   \
+            decode_half<NT, 1>(wcur, lvl, s_split, hh, hl);                                                        \
+            for (int nt = 0; nt < NT; ++nt)                                                                        \
+                wcur[nt] = load_w_rsrc<0>(wt[nt], next_, lane, col);                                               \
+            mfma_half<MT, NT, 1>(cur, ao, soff, hh, hl, d, acc);                                                   \
+        } else {                                                                                                   \
+            for (int nt = 0; nt < NT; ++nt)                                                                        \
+                wnext[nt] = load_w_rsrc<0>(wt[nt], next_, lane, col);                                              \
+            __builtin_amdgcn_sched_barrier(0);                                                                     \
+            decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);                                                       \
+            mfma_block<MT, NT>(cur, ao, soff, bh, bl, d, acc);                                                     \
+            for (int nt = 0; nt < NT; ++nt)                                                                        \
+                wcur[nt] = wnext[nt];                                                                              \
+        }                                                                                                          \
         __syncthreads();                                                                                           \
     } while (0)
     for (int b = b0; b < b1; ++b) {
@@ -1457,12 +1517,12 @@ template <int MT, int NT, int W>
 void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
                     int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
-    if constexpr (MT >= 16)
+    if constexpr (MT >= 16 && W <= 8) // 256 x 128 x 8: register staging
         hipLaunchKernelGGL((gemm_tiled_regs_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv,
                            ldxv, xs, ldxs, M, ga, B, bps, atomic);
-    else
-        hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs, ldxs, M, ga,
-                           B, bps, atomic);
+    else // direct copies; 256 x 256 x 16 in the half-K form
+        hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W, (MT >= 16)>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs,
+                           ldxs, M, ga, B, bps, atomic);
 }
 
 // Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves).
@@ -1474,7 +1534,7 @@ int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const
         launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                          \
         return MAMBO_OK;                                                                                           \
     }
-    MAMBO_T(16, 1, 8) MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
+    MAMBO_T(16, 1, 16) MAMBO_T(16, 1, 8) MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
     MAMBO_T(4, 2, 8) MAMBO_T(4, 2, 4) MAMBO_T(4, 1, 8) MAMBO_T(4, 1, 4)
 #undef MAMBO_T
     return mambo_fail(MAMBO_ERR_VALUE, "tiled kernel: no build for tile_m=%d, tile_n=%d, waves=%d", 16 * mt,
@@ -1531,11 +1591,14 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
                : m < kTiledMinM          ? MAMBO_GEMM_DENSE
                                          : MAMBO_GEMM_TILED;
     if (c.kernel == MAMBO_GEMM_TILED) {
-        // 128 tokens x 128 weight rows x 8 waves when that gives every CU a workgroup
-        // (measured on gfx950 over the 8B and 70B projections at 512-8192 tokens: the
-        // fastest tile or within 3% of it, ahead of 256 x 128 x 8 by up to 16% where that
-        // grid ends in a partial round), then 64 x 128 x 8; when even that leaves CUs idle,
-        // K is split (at least 8 blocks per split) until the grid covers the chip twice.
+        // 256 tokens x 256 weight rows x 16 waves (one workgroup per CU, half-K form) when
+        // that gives at least 7/8 of the CUs a workgroup (measured on gfx950: 6-17% ahead of
+        // 128 x 128 x 8 on the 8B/70B gate/up and down projections at 512-8192 tokens,
+        // behind it on grids of 192 workgroups); else 128 tokens x 128 weight rows x 8
+        // waves when that gives every CU a workgroup (the fastest of the 8-wave tiles or
+        // within 3% of it, ahead of 256 x 128 x 8 by up to 16% where that grid ends in a
+        // partial round), then 64 x 128 x 8; when even that leaves CUs idle, K is split
+        // (at least 8 blocks per split) until the grid covers the chip twice.
         // On long K (at least 48 blocks: the down projections) the 128-token tile stays
         // and K is split (at least 16 blocks per split) until the grid covers the chip
         // twice (measured: 8192 x 28672 at 256 and 512 tokens, 4096 x 14336 at 512,
@@ -1548,8 +1611,13 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         // (the 128-token tile only where its token padding is within 1/8 of the 64-token
         // tile's: never for M < 128)
         const bool fits128 = m >= 128 && cdiv(m, 128) * 128 * 8 <= cdiv(m, 64) * 64 * 9;
+        const bool fits256 = m >= 256 && cdiv(m, 256) * 256 * 8 <= cdiv(m, 128) * 128 * 9;
         const bool long_k = blocks >= 48;
-        if (fits128 && ((wgs = cdiv(rt, 8) * cdiv(m, 128)) >= kCUs || long_k)) {
+        if (fits256 && (wgs = cdiv(rt, 16) * cdiv(m, 256)) >= kCUs * 7 / 8) {
+            c.tile_m = 256;
+            c.tile_n = 256;
+            c.waves = 16;
+        } else if (fits128 && ((wgs = cdiv(rt, 8) * cdiv(m, 128)) >= kCUs || long_k)) {
             c.tile_m = 128;
             if (long_k && wgs < 2 * kCUs)
                 c.split_k = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv(2 * kCUs, wgs), blocks / 16));
@@ -1637,11 +1705,14 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
     if (cfg->kernel == MAMBO_GEMM_TILED) {
         MAMBO_REQUIRE(cfg->tile_m == 64 || cfg->tile_m == 128 || cfg->tile_m == 256, MAMBO_ERR_VALUE,
                       "tiled: tile_m must be 64, 128 or 256");
-        MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8, MAMBO_ERR_VALUE, "tiled: waves must be 4 or 8");
+        MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8 || (cfg->waves == 16 && cfg->tile_m == 256), MAMBO_ERR_VALUE,
+                      "tiled: waves must be 4 or 8 (16 only with tile_m=256)");
         MAMBO_REQUIRE(cfg->tile_n == 16 * cfg->waves || cfg->tile_n == 32 * cfg->waves, MAMBO_ERR_VALUE,
                       "tiled: tile_n must be 16 or 32 weight rows per wave");
-        MAMBO_REQUIRE(cfg->tile_m != 256 || (cfg->waves == 8 && cfg->tile_n == 128), MAMBO_ERR_VALUE,
-                      "tiled: tile_m=256 is built for 8 waves of 16 weight rows (tile_n=128)");
+        MAMBO_REQUIRE(cfg->tile_m != 256 || (cfg->waves == 8 && cfg->tile_n == 128) ||
+                          (cfg->waves == 16 && cfg->tile_n == 256),
+                      MAMBO_ERR_VALUE,
+                      "tiled: tile_m=256 is built for 8 or 16 waves of 16 weight rows (tile_n=128 or 256)");
         MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                       "split_k must be in [1, K/256]");
         return MAMBO_OK;

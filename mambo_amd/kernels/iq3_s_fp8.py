@@ -275,6 +275,8 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
         shapes = [(tile_m, waves, rows) for tile_m in (64, 128) for waves in (4, 8) for rows in (16, 32)]
         if m >= 128:
             shapes.append((256, 8, 16))
+        if m >= 256:
+            shapes.append((256, 16, 16))
         for tile_m, waves, rows_per_wave in shapes:
             for split in (1, 2, 4):
                 if split <= blocks:

@@ -83,16 +83,19 @@ def test_gemm_config_defaults_and_validation():
     ok = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 128,
                                        "tile_n": 128})
     assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(ok)) == 0
-    for bad_fields in ({"tile_m": 96}, {"waves": 2, "tile_n": 32}, {"tile_n": 96}, {"split_k": 5}):
+    for bad_fields in ({"tile_m": 96}, {"waves": 2, "tile_n": 32}, {"tile_n": 96}, {"split_k": 5},
+                       {"waves": 16, "tile_n": 256}):
         bad = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 1, "tile_m": 128,
                                             "tile_n": 128, **bad_fields})
         assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(bad)) == _native.MAMBO_ERR_VALUE, bad_fields
     split = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "waves": 4, "split_k": 4, "tile_m": 128,
                                           "tile_n": 128})
     assert lib.mambo_gemm_check_config(256, 64, 4, ctypes.byref(split)) == 0
-    # 256 tokens: built for 8 waves of 16 weight rows only
-    for fields, rc in (({"waves": 8, "tile_n": 128}, 0), ({"waves": 4, "tile_n": 64}, _native.MAMBO_ERR_VALUE),
-                       ({"waves": 8, "tile_n": 256}, _native.MAMBO_ERR_VALUE)):
+    # 256 tokens: built for 8 or 16 waves of 16 weight rows only; 16 waves only there
+    for fields, rc in (({"waves": 8, "tile_n": 128}, 0), ({"waves": 16, "tile_n": 256}, 0),
+                       ({"waves": 4, "tile_n": 64}, _native.MAMBO_ERR_VALUE),
+                       ({"waves": 8, "tile_n": 256}, _native.MAMBO_ERR_VALUE),
+                       ({"waves": 16, "tile_n": 512}, _native.MAMBO_ERR_VALUE)):
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "split_k": 1, "tile_m": 256, **fields})
         assert lib.mambo_gemm_check_config(2048, 4096, 16, ctypes.byref(c)) == rc, fields
     # dense default: 32 tokens per workgroup above 16 tokens; tiles per workgroup by grid size
@@ -105,20 +108,24 @@ def test_gemm_config_defaults_and_validation():
                        ({"tile_m": 48, "waves": 4}, _native.MAMBO_ERR_VALUE)):
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_DENSE, "split_k": 1, **fields})
         assert lib.mambo_gemm_check_config(32, 4096, 16, ctypes.byref(c)) == rc, fields
-    # prefill default: 128 x 128 x 8 when that still gives every CU a workgroup (and pads
-    # the tokens by at most 1/8 more than 64-token tiles), else 64 x 128 x 8; on long K
-    # (>= 48 blocks) the 128-token tile with K split until the grid covers the chip twice
-    for m, n, blocks, tile, split in ((2048, 4096, 32, (128, 128), 1), (8192, 14336, 32, (128, 128), 1),
-                                      (512, 8192, 32, (128, 128), 1), (512, 57344, 32, (128, 128), 1),
-                                      (256, 8192, 32, (64, 128), 1), (64, 57344, 32, (64, 128), 1),
-                                      (128, 57344, 32, (128, 128), 1), (384, 57344, 32, (128, 128), 1),
-                                      (192, 57344, 32, (64, 128), 1), (256, 8192, 112, (128, 128), 4),
-                                      (512, 8192, 112, (128, 128), 2), (2048, 8192, 112, (128, 128), 1),
-                                      (512, 4096, 56, (128, 128), 3), (128, 8192, 112, (128, 128), 7)):
+    # prefill default: 256 x 256 x 16 waves when that gives at least 7/8 of the CUs a
+    # workgroup (and pads the tokens by at most 1/8 more than 128-token tiles), else
+    # 128 x 128 x 8 when that gives every CU a workgroup (padding at most 1/8 over 64-token
+    # tiles), else 64 x 128 x 8; on long K (>= 48 blocks) the 128-token tile with K split
+    # until the grid covers the chip twice
+    for m, n, blocks, tile, split in ((2048, 4096, 32, (128, 128, 8), 1), (8192, 14336, 32, (256, 256, 16), 1),
+                                      (512, 8192, 32, (128, 128, 8), 1), (512, 57344, 32, (256, 256, 16), 1),
+                                      (512, 28672, 16, (256, 256, 16), 1), (2048, 6144, 16, (128, 128, 8), 1),
+                                      (256, 8192, 32, (64, 128, 8), 1), (64, 57344, 32, (64, 128, 8), 1),
+                                      (128, 57344, 32, (128, 128, 8), 1), (384, 57344, 32, (128, 128, 8), 1),
+                                      (192, 57344, 32, (64, 128, 8), 1), (256, 8192, 112, (128, 128, 8), 4),
+                                      (512, 8192, 112, (128, 128, 8), 2), (2048, 8192, 112, (256, 256, 16), 1),
+                                      (512, 4096, 56, (128, 128, 8), 3), (128, 8192, 112, (128, 128, 8), 7)):
         c = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(m, n, blocks, ctypes.byref(c)) == 0
-        assert (c.kernel, c.tile_m, c.tile_n, c.waves, c.split_k) == (_native.GEMM_TILED, *tile, 8, split), \
+        assert (c.kernel, c.tile_m, c.tile_n, c.waves, c.split_k) == (_native.GEMM_TILED, *tile, split), \
             (m, n, blocks, c.as_dict())
+        assert lib.mambo_gemm_check_config(m, n, blocks, ctypes.byref(c)) == 0
     # moderate M on a long K: the tiled default splits K to fill the chip
     c = _native.GemmConfig()
     assert lib.mambo_gemm_default_config(64, 8192, 112, ctypes.byref(c)) == 0

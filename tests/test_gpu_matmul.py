@@ -304,7 +304,7 @@ def test_tiled_kernel_every_tile_shape(gpu, m):
     expected = oracle.iq3s_fp8_matmul(xv, xs, raw, threads=oracle.default_threads())
     xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
     shapes = [(tile_m, waves, rows) for tile_m in (64, 128) for waves in (4, 8) for rows in (16, 32)]
-    shapes.append((256, 8, 16))
+    shapes += [(256, 8, 16), (256, 16, 16)]
     for tile_m, waves, rows_per_wave in shapes:
         cfg = {"kernel": _native.GEMM_TILED, "waves": waves, "split_k": 1 if m != 100 else 3,
                "tile_m": tile_m, "tile_n": rows_per_wave * waves}
