@@ -1592,7 +1592,7 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
                                          : MAMBO_GEMM_TILED;
     if (c.kernel == MAMBO_GEMM_TILED) {
         // 256 tokens x 256 weight rows x 16 waves (one workgroup per CU, half-K form) when
-        // that gives at least 7/8 of the CUs a workgroup (measured on gfx950: 6-17% ahead of
+        // every round of its grid fills at least 7/8 of the CUs (measured on gfx950: 6-17% ahead of
         // 128 x 128 x 8 on the 8B/70B gate/up and down projections at 512-8192 tokens,
         // behind it on grids of 192 workgroups); else 128 tokens x 128 weight rows x 8
         // waves when that gives every CU a workgroup (the fastest of the 8-wave tiles or
@@ -1613,7 +1613,10 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         const bool fits128 = m >= 128 && cdiv(m, 128) * 128 * 8 <= cdiv(m, 64) * 64 * 9;
         const bool fits256 = m >= 256 && cdiv(m, 256) * 256 * 8 <= cdiv(m, 128) * 128 * 9;
         const bool long_k = blocks >= 48;
-        if (fits256 && (wgs = cdiv(rt, 16) * cdiv(m, 256)) >= kCUs * 7 / 8) {
+        // (one workgroup per CU: rounds must be nearly full - 320 workgroups run as two
+        // rounds, and 128 x 128 x 8 was 18% faster there)
+        if (fits256 && (wgs = cdiv(rt, 16) * cdiv(m, 256)) >= kCUs * 7 / 8 &&
+            wgs * 8 >= cdiv(wgs, kCUs) * kCUs * 7) {
             c.tile_m = 256;
             c.tile_n = 256;
             c.waves = 16;

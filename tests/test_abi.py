@@ -108,14 +108,16 @@ def test_gemm_config_defaults_and_validation():
                        ({"tile_m": 48, "waves": 4}, _native.MAMBO_ERR_VALUE)):
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_DENSE, "split_k": 1, **fields})
         assert lib.mambo_gemm_check_config(32, 4096, 16, ctypes.byref(c)) == rc, fields
-    # prefill default: 256 x 256 x 16 waves when that gives at least 7/8 of the CUs a
-    # workgroup (and pads the tokens by at most 1/8 more than 128-token tiles), else
+    # prefill default: 256 x 256 x 16 waves when every round of its grid (one workgroup
+    # per CU) fills at least 7/8 of the CUs (and the tokens are padded by at most 1/8 more
+    # than with 128-token tiles), else
     # 128 x 128 x 8 when that gives every CU a workgroup (padding at most 1/8 over 64-token
     # tiles), else 64 x 128 x 8; on long K (>= 48 blocks) the 128-token tile with K split
     # until the grid covers the chip twice
     for m, n, blocks, tile, split in ((2048, 4096, 32, (128, 128, 8), 1), (8192, 14336, 32, (256, 256, 16), 1),
                                       (512, 8192, 32, (128, 128, 8), 1), (512, 57344, 32, (256, 256, 16), 1),
                                       (512, 28672, 16, (256, 256, 16), 1), (2048, 6144, 16, (128, 128, 8), 1),
+                                      (2048, 10240, 32, (128, 128, 8), 1), (8192, 10240, 32, (256, 256, 16), 1),
                                       (256, 8192, 32, (64, 128, 8), 1), (64, 57344, 32, (64, 128, 8), 1),
                                       (128, 57344, 32, (128, 128, 8), 1), (384, 57344, 32, (128, 128, 8), 1),
                                       (192, 57344, 32, (64, 128, 8), 1), (256, 8192, 112, (128, 128, 8), 4),
