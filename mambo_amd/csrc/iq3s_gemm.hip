@@ -1562,9 +1562,22 @@ constexpr int64_t kStreamWgs = 512;
 constexpr int64_t kTiledMinM = 64;
 // Dynamic LDS per workgroup (the static codebook tables add 2.3 KiB).
 #ifndef MAMBO_MAX_DYN_LDS_KB
-#define MAMBO_MAX_DYN_LDS_KB 60
+#define MAMBO_MAX_DYN_LDS_KB 150
 #endif
 constexpr int kMaxDynLds = MAMBO_MAX_DYN_LDS_KB * 1024;
+// LDS per CU on gfx950.
+constexpr int kLdsPerCU = 160 * 1024;
+
+// Whether the stream kernel stages its chunk's activations in LDS (`lds_bytes`: the
+// workgroup's whole dynamic LDS with them): when they take at most kMaxLdsAct, or when
+// the LDS still leaves room for 16 waves per CU (one 16-wave workgroup, two 8-wave ones).
+// Beyond that they are read from L2 in the weight ring.
+bool stream_stages_act(int64_t act_bytes, int lds_bytes, int waves)
+{
+    if (lds_bytes > kMaxDynLds)
+        return false;
+    return act_bytes <= kMaxLdsAct || (int64_t)lds_bytes * 16 <= (int64_t)kLdsPerCU * waves;
+}
 
 bool valid_waves(int w)
 {
@@ -1677,6 +1690,15 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         // several tiles per CU (measured on gfx950 at M = 1 and 4: 7 tiles per workgroup
         // for 3584 tiles, 4 for 1792, 1 for 512-640).
         c.tile_n = (int32_t)(kTileRows * std::max<int64_t>(1, (units + kStreamWgs / 2) / kStreamWgs));
+        // Activations past kMaxLdsAct (M = 2..4 on K = 14K-28K): one 16-wave workgroup per
+        // CU stages them once for all its waves (measured on the 70B down projection
+        // 8192 x 28672: 21.3 / 22.4 / 24.1 us at M = 2 / 3 / 4 against 26-28 us with them
+        // read from L2 in the ring).
+        const int64_t act = std::min<int64_t>(16, m) * blocks * 256 * 33 / 32;
+        if (act > kMaxLdsAct && blocks >= 32 && act + 8192 <= kMaxDynLds) {
+            waves = 16;
+            c.tile_n = (int32_t)(kTileRows * std::max<int64_t>(1, (units + kCUs / 2) / kCUs));
+        }
     }
     int64_t split = 1;
     if (units * waves < (c.kernel == MAMBO_GEMM_DENSE ? kMinWaves / 4 : kMinWaves)) {
@@ -1859,8 +1881,8 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         rc = launch_dense(c.waves, nt, mc, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, gd, B, bps, atomic);
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
-        if (lds_act && stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total > kMaxDynLds)
-            lds_act = false;
+        lds_act = stream_stages_act((int64_t)rows * k * 33 / 32,
+                                    stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves);
         // the staging copies move activation scales as dwords
         if ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0)
             lds_act = false;
