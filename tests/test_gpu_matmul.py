@@ -162,6 +162,34 @@ def test_llama3_70b_gate_shape_sampled(gpu, m):
     check(out[:, rows], expected, elementwise=False)
 
 
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_llama3_70b_down_shape_staged_rows(gpu, m):
+    """8192 x 28672 (down) at 2-4 tokens: 57-115 KiB of activation rows, staged in LDS for
+    one 16-wave workgroup per CU by the default configuration (and, as a check of the
+    other form, read from L2 by an 8-wave configuration); sampled rows against the
+    oracle."""
+    import ctypes
+
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    n, k = 8192, 28672
+    c = _native.GemmConfig()
+    assert _native.lib().mambo_gemm_default_config(m, n, k // 256, ctypes.byref(c)) == 0
+    assert (c.kernel, c.waves) == (_native.GEMM_STREAM, 16), c.as_dict()
+    step(f"synth weight {n}x{k}")
+    fields = _synth_weight(gpu, n, k, seed=6)
+    xq, xs = launch_quantize_fp8(_synth_act(gpu, m, k, seed=10 + m))
+    rows = np.sort(np.random.default_rng(2).choice(n, 128, replace=False))
+    raw = np.concatenate([oracle.gen_iq3s(6, 1, k // 256, row0=int(r)) for r in rows])
+    expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
+    for cfg in (c.as_dict(), {"kernel": _native.GEMM_STREAM, "waves": 8, "split_k": 1, "tile_n": 16}):
+        step(f"matmul M={m} {n}x{k} cfg={cfg}")
+        out = launch_iq3_s_fp8_matmul(xq, xs, fields, config=cfg).cpu().numpy()
+        torch.cuda.synchronize()
+        check(out[:, rows], expected, elementwise=False)
+
+
 def test_graph_capture_replays_match_eager(gpu):
     """Split-K launches (zero-fill kernel + atomics) captured in a HIP graph: every replay,
     with eager work between replays, matches the eager result."""
