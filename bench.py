@@ -20,7 +20,8 @@ peak instead. cpu_baseline: the oracle's restatement of the reference CPU path
 (ggml_reference.cpp:495-523: IQ3_S to_float + float64 dot) on its CPU case, one IQ3_S
 linear N=K=4096 with M=8, timed on this host.
 
-    python bench.py [--steps K] [--warmup W] [--m M] [--workload llama70b|llama8b|quant|copy]
+    python bench.py [--steps K] [--warmup W] [--m M]
+                    [--workload llama70b|llama8b|quant|copy|read|readsweep|mfma]
                     [--layers L] [--no-group] [--no-graph]
 """
 
@@ -316,6 +317,71 @@ def run_read(args):
             "per_launch_bytes": COPY_BYTES, "per_launch_us": ms * 1e3}
 
 
+def sweep_launch_bytes(args) -> list:
+    """Packed IQ3_S bytes each launch of the projection sweep reads (the grouping of
+    build_gemm_workload: q/k/v and gate/up share a launch unless args.no_group)."""
+    shapes = LLAMA70B_LAYER if args.workload in ("llama70b", "readsweep") else LLAMA8B_LAYER
+    sizes = []
+    for _ in range(args.layers):
+        prev = None
+        for _, n, k, slot in shapes:
+            nbytes = n * (k // 256) * 110
+            if not args.no_group and prev == slot and len(sizes[-1]) < 4:
+                sizes[-1].append(nbytes)
+            else:
+                sizes.append([nbytes])
+            prev = slot
+    return [sum(s) for s in sizes]
+
+
+def run_readsweep(args):
+    """Plain read (mambo_read_bytes) of one buffer per launch of the Llama-3-70B sweep, each
+    the size of the packed weights that launch streams, replayed from a HIP graph: the
+    ceiling a weight stream with this launch structure can reach on this device (per-launch
+    ramp-up and drain included). The last buffer's read is checked against its XOR."""
+    import numpy as np
+    import torch
+    from mambo_amd import _native
+    sizes = sweep_launch_bytes(args)
+    bufs = [torch.empty(s, dtype=torch.uint8, device="cuda") for s in sizes]
+    sink = torch.empty(_native.READ_SINK_WORDS, dtype=torch.int32, device="cuda")
+    log(f"{len(sizes)} launches, {sum(sizes) / 1e9:.2f} GB resident")
+
+    def step():
+        for b, s in zip(bufs, sizes):
+            _native.check(_native.lib().mambo_read_bytes(b.data_ptr(), s, sink.data_ptr(),
+                                                         _native.stream_handle(None)), "read")
+
+    step()
+    torch.cuda.synchronize()
+    words = bufs[-1].view(torch.int32).cpu().numpy()
+    if int(np.bitwise_xor.reduce(sink.cpu().numpy())) != int(np.bitwise_xor.reduce(words)):
+        raise RuntimeError("read kernel returned a wrong checksum")
+    replay = step
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(graph, stream=side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        replay = graph.replay
+    for _ in range(args.warmup):
+        replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    total = sum(sizes)
+    log(f"{ms:.3f} ms/step, {total / (ms * 1e-3) / 1e9:.1f} GB/s")
+    return {"ms": ms, "value": total / (ms * 1e-3) / 1e9, "step_bytes": total, "launches": len(sizes),
+            "per_launch_bytes": total / len(sizes), "per_launch_us": ms * 1e3 / len(sizes)}
+
+
 MFMA_WORKGROUPS = 1024  # x 4 waves: 4 waves per SIMD on 256 CUs
 MFMA_ITERS = 20000
 
@@ -364,7 +430,7 @@ def main(argv=None) -> int:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--m", type=int, default=1, help="tokens per projection")
-    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy", "read", "mfma"],
+    p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy", "read", "readsweep", "mfma"],
                    default="llama70b")
     p.add_argument("--layers", type=int, default=None, help="layers in the sweep (default 80 for llama70b, 32 for llama8b)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -400,6 +466,15 @@ def main(argv=None) -> int:
         workload = f"read {COPY_BYTES} bytes"
         config = {"workload": workload}
         dtype, data = "u8", "synthetic bytes"
+    elif args.workload == "readsweep":
+        r = run_readsweep(args)
+        metric = "plain device read GB/s over the llama3-70b sweep's launch sizes (weight-stream ceiling)"
+        grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
+        workload = (f"read the packed IQ3_S bytes of llama3-70b's {args.layers} layers x 7 linears, one buffer "
+                    f"per launch, {grouping}")
+        config = {"workload": workload, "launches_per_step": r["launches"],
+                  "bytes_gb": round(r["step_bytes"] / 1e9, 3), "graph": not args.no_graph}
+        dtype, data = "u8", "uninitialised device bytes"
     elif args.workload == "mfma":
         r = run_mfma(args)
         metric = "scaled MFMA f8f6f4 16x16x128 TFLOP/s (device check of the MX-FP8 peak)"

@@ -159,6 +159,14 @@ int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_c
 /* Validates cfg for the shape (MAMBO_OK or MAMBO_ERR_VALUE with a reason). */
 int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, const mambo_gemm_config *cfg);
 
+/* Autotuner candidates for the shape (replaces the search-space construction of
+ * make_benchmark_cases, iq3_s_fp8.py:402-465): writes the first min(count, capacity)
+ * configurations to out (out may be NULL when capacity is 0) and returns count, or a
+ * negative status. out[0] is the library default (all fields 0, MAMBO_GEMM_AUTO); every
+ * other entry passes mambo_gemm_check_config for (m, n, blocks). */
+int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out,
+                                    int64_t capacity);
+
 /* Synthetic inputs for benchmarks and full-size checks (no reference counterpart; the
  * reference draws them with numpy/cupy RNGs, test_iq3_s_fp8.py:41-51). Counter-based:
  *   rnd(seed, stream, i) = splitmix64(splitmix64(seed*0xD1B54A32D192ED03 + stream) + i);

@@ -87,6 +87,7 @@ SIGNATURES = {
                                              ctypes.POINTER(GemmConfig), _vp]),
     "mambo_gemm_default_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_gemm_check_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
+    "mambo_gemm_config_enumerate": (_i64, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig), _i64]),
     "mambo_synth_iq3s": (_i32, [_u64, _i64, _i64, _i64, _vp, _vp]),
     "mambo_synth_bf16": (_i32, [_u64, _u64, ctypes.c_double, _i64, _i64, _vp, _vp]),
     "mambo_e4m3_convert": (_i32, [_vp, _i64, _vp, _vp, _vp]),

@@ -1758,6 +1758,75 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
     return MAMBO_OK;
 }
 
+// Autotuner candidates for one shape (the analogue of the search spaces built in
+// iq3_s_fp8.py:416-459), led by the library default (an all-zero MAMBO_GEMM_AUTO entry):
+// the stream kernel up to 16 tokens and the dense kernel up to 128 (both re-read every
+// weight once per 16- or 32-token chunk, so neither is a candidate beyond), each over
+// waves per workgroup x K split x weight rows (and, dense above 16 tokens, tokens) per
+// workgroup; from 32 tokens the tiled kernel's tile shapes x K split. Every entry but the
+// first passes mambo_gemm_check_config for the shape.
+extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out,
+                                               int64_t capacity)
+{
+    MAMBO_REQUIRE(m >= 1 && n >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive");
+    MAMBO_REQUIRE(capacity >= 0 && (out != nullptr || capacity == 0), MAMBO_ERR_VALUE,
+                  "out must hold capacity configurations");
+    int64_t count = 0;
+    auto add = [&](int32_t kernel, int32_t waves, int32_t split, int32_t tile_m, int32_t tile_n) {
+        if (count < capacity) {
+            mambo_gemm_config c = {};
+            c.kernel = kernel;
+            c.waves = waves;
+            c.split_k = split;
+            c.tile_m = tile_m;
+            c.tile_n = tile_n;
+            out[count] = c;
+        }
+        ++count;
+    };
+    add(MAMBO_GEMM_AUTO, 0, 0, 0, 0);
+    const int64_t u = std::min<int64_t>(4, cdiv(m, 4)); // 4-token sub-tiles of the stream kernel
+    static const int32_t kWaves[] = {1, 2, 4, 6, 8, 12, 16};
+    static const int32_t kSplits[] = {1, 2, 4, 8};
+    for (const int32_t kernel : {MAMBO_GEMM_STREAM, MAMBO_GEMM_DENSE}) {
+        if (m > (kernel == MAMBO_GEMM_STREAM ? 16 : 128))
+            continue;
+        for (const int32_t waves : kWaves) {
+            if (waves > blocks || (kernel == MAMBO_GEMM_STREAM && waves * u > 32))
+                continue;
+            for (const int32_t split : kSplits) {
+                if (split > blocks / waves)
+                    continue;
+                if (kernel == MAMBO_GEMM_STREAM) { // runs of 1..8 tiles per workgroup
+                    for (const int32_t rows : {16, 32, 64, 128})
+                        if (split == 1 || rows == 16)
+                            add(kernel, waves, split, 0, rows);
+                } else { // tiles sharing one activation fragment, tokens per workgroup
+                    const bool two_chunks = m > 16 && (waves == 2 || waves == 4 || waves == 8);
+                    for (const int32_t rows : {16, 32, 64})
+                        for (const int32_t tokens : {16, 32})
+                            if ((tokens == 16 || two_chunks) && waves * rows * tokens / 16 <= 256)
+                                add(kernel, waves, split, tokens, rows);
+                }
+            }
+        }
+    }
+    if (m >= 32) { // tokens x weight rows per wave x waves
+        for (const int32_t tile_m : {64, 128, 256})
+            for (const int32_t waves : {4, 8, 16})
+                for (const int32_t rows : {16, 32}) {
+                    const bool built = tile_m == 256 ? rows == 16 && ((waves == 8 && m >= 128) || (waves == 16 && m >= 256))
+                                                     : waves != 16;
+                    if (!built)
+                        continue;
+                    for (const int32_t split : {1, 2, 4})
+                        if (split <= blocks)
+                            add(MAMBO_GEMM_TILED, waves, split, tile_m, rows * waves);
+                }
+    }
+    return count;
+}
+
 namespace {
 
 int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t m,

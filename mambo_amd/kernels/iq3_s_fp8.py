@@ -246,42 +246,31 @@ def launch_iq3_s_fp8_matmul_grouped(x_values: torch.Tensor, x_scales: torch.Tens
 
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
-    search spaces of iq3_s_fp8.py:416-459), led by the library default for the token
-    count: the block-diagonal stream kernel up to 16 tokens and the dense kernel up to
-    128 (each re-reads every weight once per 16- or 32-token chunk, so neither is a
-    candidate beyond), x waves per workgroup x K split x weight rows (and, dense above 16
-    tokens, tokens) per workgroup; for M >= 32 the tiled kernel's tile shapes."""
+    search spaces of iq3_s_fp8.py:416-459), as mambo_gemm_config_enumerate lists them:
+    led by the library default for the token count, then the block-diagonal stream kernel
+    up to 16 tokens and the dense kernel up to 128 (each re-reads every weight once per
+    16- or 32-token chunk, so neither is a candidate beyond), x waves per workgroup x K
+    split x weight rows (and, dense above 16 tokens, tokens) per workgroup; for M >= 32
+    the tiled kernel's tile shapes."""
+    if k % IQ3_S_BLOCK_VALUES:
+        raise ValueError(f"K={k} must be a multiple of {IQ3_S_BLOCK_VALUES}")
+    lib = _native.lib()
     blocks = k // IQ3_S_BLOCK_VALUES
-    u = min(4, -(-m // 4))
-    space = [default_config(m)]
-    families = [kern for kern, limit in ((_native.GEMM_STREAM, 16), (_native.GEMM_DENSE, 128)) if m <= limit]
-    for kernel in families:
-        for waves in (1, 2, 4, 6, 8, 12, 16):
-            if waves > blocks or (kernel == _native.GEMM_STREAM and waves * u > 32):
-                continue
-            for split in (1, 2, 4, 8):
-                if split > blocks // waves:
-                    continue
-                if kernel == _native.GEMM_STREAM:  # runs of 1..8 tiles per workgroup
-                    for rows in ((16, 32, 64, 128) if split == 1 else (16,)):
-                        space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows})
-                else:  # weight tiles per workgroup sharing one activation fragment, tokens per workgroup
-                    for rows in (16, 32, 64):
-                        for tokens in ((16, 32) if m > 16 and waves in (2, 4, 8) else (16,)):
-                            if waves * rows * tokens // 16 <= 256:
-                                space.append({"kernel": kernel, "waves": waves, "split_k": split, "tile_n": rows,
-                                              "tile_m": tokens})
-    if m >= 32:  # tiled kernel: tokens x (weight rows per wave) x waves per workgroup x K split
-        shapes = [(tile_m, waves, rows) for tile_m in (64, 128) for waves in (4, 8) for rows in (16, 32)]
-        if m >= 128:
-            shapes.append((256, 8, 16))
-        if m >= 256:
-            shapes.append((256, 16, 16))
-        for tile_m, waves, rows_per_wave in shapes:
-            for split in (1, 2, 4):
-                if split <= blocks:
-                    space.append({"kernel": _native.GEMM_TILED, "waves": waves, "split_k": split,
-                                  "tile_m": tile_m, "tile_n": rows_per_wave * waves})
+    count = lib.mambo_gemm_config_enumerate(m, n, blocks, None, 0)
+    if count < 0:
+        _native.check(int(count), "gemm_search_space")
+    configs = (_native.GemmConfig * count)()
+    _native.check(0 if lib.mambo_gemm_config_enumerate(m, n, blocks, configs, count) == count else -1,
+                  "gemm_search_space")
+    space = []
+    for c in configs:
+        if c.kernel == _native.GEMM_AUTO:
+            space.append(default_config(m))
+        elif c.kernel == _native.GEMM_STREAM:
+            space.append({"kernel": c.kernel, "waves": c.waves, "split_k": c.split_k, "tile_n": c.tile_n})
+        else:
+            space.append({"kernel": c.kernel, "waves": c.waves, "split_k": c.split_k, "tile_n": c.tile_n,
+                          "tile_m": c.tile_m})
     return space
 
 

@@ -131,6 +131,33 @@ def test_search_space_families_and_validity():
                 assert lib.mambo_gemm_check_config(m, n, k // 256, ctypes.byref(cfg)) == 0, (m, n, k, c)
 
 
+def test_config_enumerate_abi():
+    """mambo_gemm_config_enumerate: a count query with no buffer, a truncated write that
+    leaves the rest of the buffer alone, the default (all zero) first, and status codes
+    for bad arguments (no launches)."""
+    import ctypes
+
+    from mambo_amd import _native
+    lib = _native.lib()
+    m, n, blocks = 4, 8192, 32
+    count = lib.mambo_gemm_config_enumerate(m, n, blocks, None, 0)
+    assert count > 1
+    full = (_native.GemmConfig * count)()
+    assert lib.mambo_gemm_config_enumerate(m, n, blocks, full, count) == count
+    assert full[0].as_dict() == {"kernel": 0, "waves": 0, "split_k": 0, "tile_m": 0, "tile_n": 0}
+    part = (_native.GemmConfig * 4)()
+    for c in part:
+        c.kernel = 99
+    assert lib.mambo_gemm_config_enumerate(m, n, blocks, part, 3) == count
+    assert [c.as_dict() for c in part[:3]] == [c.as_dict() for c in full[:3]]
+    assert part[3].kernel == 99
+    assert lib.mambo_gemm_config_enumerate(0, n, blocks, None, 0) == _native.MAMBO_ERR_VALUE
+    assert "positive" in lib.mambo_last_error().decode()
+    assert lib.mambo_gemm_config_enumerate(m, n, blocks, None, 5) == _native.MAMBO_ERR_VALUE
+    assert lib.mambo_gemm_config_enumerate(m, n, blocks, ctypes.cast(part, ctypes.POINTER(_native.GemmConfig)),
+                                           -1) == _native.MAMBO_ERR_VALUE
+
+
 def test_tuned_table_drops_shapes_the_default_won(tmp_path, monkeypatch):
     from mambo_amd.kernels import iq3_s_fp8
     from mambo_amd.utils.kernel_benchmark import TuneResult, write_tuned_table
