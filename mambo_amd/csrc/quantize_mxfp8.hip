@@ -20,6 +20,11 @@ namespace {
 // |x * 2^-e| <= 448.
 constexpr bool kQuantHwCvt = true;
 
+// Rows per workgroup iteration: the loads of both rows are issued before either is
+// converted, two 16-byte loads in flight per lane ([4096,4096] bf16: 4345 -> 4565 GB/s;
+// 4 and 8 rows, with a quarter / eighth of the workgroups, measured 6% and 16% slower).
+constexpr int kQuantRows = 2;
+
 // The input is read once and the codes written once: both go through with the
 // non-temporal hint (bf16 [4096,4096] from a HIP graph: 3.89 -> 4.34 TB/s).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -79,53 +84,58 @@ __global__ __launch_bounds__(256) void quantize_mxfp8_kernel(const void *__restr
     const int64_t g = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
     const int j = threadIdx.x & 3;
     const bool ok = g < groups;
-    for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
-        float v[8];
-        if (ok) {
-            const int64_t off = row * ldx + 32 * g + 8 * j;
-            if constexpr (kVec)
-                load8<kBf16>(x, off, v);
-            else
-                load8_scalar<kBf16>(x, off, v);
-        } else {
+    constexpr int R = kQuantRows;
+    for (int64_t row0 = (int64_t)blockIdx.y * R; row0 < m; row0 += (int64_t)gridDim.y * R) {
+        float v[R][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                v[i] = 0.0f;
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            amax = fmaxf(amax, fabsf(v[i]));
-        // quad reduction: lanes 4t..4t+3 hold one group
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
-        const int e = mxfp8_exponent(amax);
-        if (ok) {
-            float y[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                y[i] = __builtin_ldexpf(v[i], -e); // exact scaling by a power of two
-            uint2 out;
-            out.x = pack4<kHw>(y[0], y[1], y[2], y[3]);
-            out.y = pack4<kHw>(y[4], y[5], y[6], y[7]);
-            uint8_t *vp = values + row * ldv + 32 * g + 8 * j;
-            if constexpr (kVec) {
-                __builtin_nontemporal_store(u32x2{out.x, out.y}, reinterpret_cast<u32x2 *>(vp));
+        for (int r = 0; r < R; ++r) {
+            if (ok && row0 + r < m) {
+                const int64_t off = (row0 + r) * ldx + 32 * g + 8 * j;
+                if constexpr (kVec)
+                    load8<kBf16>(x, off, v[r]);
+                else
+                    load8_scalar<kBf16>(x, off, v[r]);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    vp[i] = (uint8_t)(out.x >> (8 * i));
-                    vp[4 + i] = (uint8_t)(out.y >> (8 * i));
-                }
+                for (int i = 0; i < 8; ++i)
+                    v[r][i] = 0.0f;
             }
-            if (j == 0)
-                scales[row * lds + g] = (uint8_t)(e + 127);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t row = row0 + r;
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                amax = fmaxf(amax, fabsf(v[r][i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1));
+            amax = fmaxf(amax, __shfl_xor(amax, 2));
+            const int e = mxfp8_exponent(amax);
+            if (ok && row < m) {
+                float y[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    y[i] = __builtin_ldexpf(v[r][i], -e); // exact scaling by a power of two
+                uint2 out;
+                out.x = pack4<kHw>(y[0], y[1], y[2], y[3]);
+                out.y = pack4<kHw>(y[4], y[5], y[6], y[7]);
+                uint8_t *vp = values + row * ldv + 32 * g + 8 * j;
+                if constexpr (kVec) {
+                    __builtin_nontemporal_store(u32x2{out.x, out.y}, reinterpret_cast<u32x2 *>(vp));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        vp[i] = (uint8_t)(out.x >> (8 * i));
+                        vp[4 + i] = (uint8_t)(out.y >> (8 * i));
+                    }
+                }
+                if (j == 0)
+                    scales[row * lds + g] = (uint8_t)(e + 127);
+            }
         }
     }
 }
 
-// Element-wise E4M3 conversion with the software and the hardware rounding paths, for
-// checking the hardware conversion against the integer restatement.
 __global__ void e4m3_convert_kernel(const float *__restrict__ in, int64_t n, uint8_t *__restrict__ sw,
                                     uint8_t *__restrict__ hw)
 {
@@ -143,7 +153,8 @@ template <bool kBf16, bool kVec>
 int launch(const void *x, int64_t m, int64_t groups, int64_t ldx, uint8_t *values, int64_t ldv,
            uint8_t *scales, int64_t lds, hipStream_t stream)
 {
-    dim3 grid((unsigned)((groups + 63) / 64), (unsigned)(m < 65535 ? m : 65535));
+    const int64_t ry = (m + kQuantRows - 1) / kQuantRows;
+    dim3 grid((unsigned)((groups + 63) / 64), (unsigned)(ry < 65535 ? ry : 65535));
     hipLaunchKernelGGL((quantize_mxfp8_kernel<kBf16, kVec, kQuantHwCvt>), grid, dim3(256), 0, stream,
                        x, ldx, m, groups, values, ldv, scales, lds);
     return mambo_check_launch("quantize_mxfp8");
