@@ -22,7 +22,7 @@ linear N=K=4096 with M=8, timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--m M]
                     [--workload llama70b|llama8b|quant|copy|read|readsweep|mfma]
-                    [--layers L] [--no-group] [--no-graph]
+                    [--layers L] [--no-group] [--no-graph] [--with-quant none|separate|fused]
 """
 
 from __future__ import annotations
@@ -51,8 +51,8 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def proj_bytes(m: int, n: int, k: int) -> int:
-    return n * k * 110 // 256 + m * k * 33 // 32 + 4 * m * n
+def proj_bytes(m: int, n: int, k: int, act_bytes_per_value: float = 33 / 32) -> int:
+    return n * k * 110 // 256 + int(m * k * act_bytes_per_value) + 4 * m * n
 
 
 def synth_weight(n: int, k: int, seed: int):
@@ -67,12 +67,14 @@ def synth_weight(n: int, k: int, seed: int):
 
 
 def synth_activation(m: int, k: int, seed: int):
+    """(E4M3 values, E8M0 scales, bf16 rows) of synthetic ~N(0,1) activations."""
     import torch
     from mambo_amd import _native
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
     bits = torch.empty(m * k, dtype=torch.int16, device="cuda")
     _native.check(_native.lib().mambo_synth_bf16(seed, 2, 0.0, 0, m * k, bits.data_ptr(), _native.stream_handle(None)))
-    return launch_quantize_fp8(bits.view(torch.bfloat16).view(m, k))
+    rows = bits.view(torch.bfloat16).view(m, k)
+    return (*launch_quantize_fp8(rows), rows)
 
 
 def build_gemm_workload(args):
@@ -113,19 +115,27 @@ def build_gemm_workload(args):
 def run_gemm(args):
     import torch
     from mambo_amd.kernels.iq3_s_fp8 import (launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped,
-                                             select_config)
+                                             launch_iq3_s_matmul_quantize, select_config)
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
 
     launches = build_gemm_workload(args)
     projections = [p for (_, projs, _) in launches for p in projs]
     configs = [select_config(args.m, sum(n for n, _, _, _ in projs), projs[0][1]) for (_, projs, _) in launches]
     weight_bytes = sum(f.packed.numel() for (_, _, f, _) in projections)
-    step_bytes = sum(proj_bytes(args.m, n, k) for (n, k, _, _) in projections)
+    # with quantization in the step the activations come in as bf16 rows
+    act_bytes = 2 if args.with_quant != "none" else 33 / 32
+    step_bytes = sum(proj_bytes(args.m, n, k, act_bytes) for (n, k, _, _) in projections)
     step_flops = sum(2 * args.m * n * k for (n, k, _, _) in projections)
     log(f"{len(projections)} projections in {len(launches)} launches, {weight_bytes / 1e9:.2f} GB of IQ3_S "
         "weights resident")
 
     def step():
-        for (_, projs, (xv, xs)), cfg in zip(launches, configs):
+        for (_, projs, (xv, xs, rows)), cfg in zip(launches, configs):
+            if args.with_quant == "fused":
+                launch_iq3_s_matmul_quantize(rows, [p[2] for p in projs], config=cfg, outs=[p[3] for p in projs])
+                continue
+            if args.with_quant == "separate":
+                launch_quantize_fp8(rows, out=(xv, xs))
             if len(projs) == 1:
                 launch_iq3_s_fp8_matmul(xv, xs, projs[0][2], config=cfg, out=projs[0][3])
             else:
@@ -434,6 +444,10 @@ def main(argv=None) -> int:
                    default="llama70b")
     p.add_argument("--layers", type=int, default=None, help="layers in the sweep (default 80 for llama70b, 32 for llama8b)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--with-quant", choices=["none", "separate", "fused"], default="none",
+                   help="time the activation quantization in the step: a quantizer launch before each GEMM "
+                        "(separate) or inside it (fused, launch_iq3_s_matmul_quantize); default: activations "
+                        "quantized once before timing, as the reference times the matmul alone")
     p.add_argument("--no-group", action="store_true",
                    help="one launch per projection (default: q/k/v and gate/up share a launch)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -492,6 +506,10 @@ def main(argv=None) -> int:
         metric = ("fused IQ3_S x MXFP8 GEMM TFLOP/s vs MX-FP8 MFMA roofline" if args.m >= PREFILL_M else
                   "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline")
         grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
+        if args.with_quant != "none":
+            metric += " (bf16 activations quantized in the step)"
+            grouping += {"separate": ", a quantizer launch before each GEMM launch",
+                         "fused": ", quantization inside the GEMM launch where it fits (M <= 4)"}[args.with_quant]
         if args.workload == "llama70b":
             workload = f"llama3-70b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
         else:

@@ -153,6 +153,20 @@ int mambo_iq3s_fp8_matmul_grouped(const uint8_t *xv, int64_t ldxv, const uint8_t
                                   int64_t m, const mambo_projection *proj, int count, int64_t blocks,
                                   const mambo_gemm_config *cfg, mambo_stream_t stream);
 
+/* Quantize + matmul in one call (no reference counterpart: the reference quantizes in a
+ * launch of its own, quantize_fp8.py:1-4, then calls iq3_s_fp8_matmul; this is the
+ * fused activation-quantize prologue for decode M). x: unquantized activations [m, K]
+ * (MAMBO_DTYPE_F32 or _BF16, row stride ldx elements); proj/count/blocks/cfg as for
+ * mambo_iq3s_fp8_matmul_grouped. For M <= 4 on the stream kernel with its rows staged in
+ * LDS (and x 16-byte aligned) every workgroup quantizes the rows into its LDS copy with
+ * the quantizer's arithmetic - one launch, results bit-identical to the two-step path
+ * with the same cfg - and xv/xs are not touched; otherwise mambo_quantize_mxfp8 writes
+ * the caller's MXFP8 buffers xv [m, ldxv] / xs [m, ldxs] and the GEMM reads them. */
+int mambo_iq3s_matmul_quantize_grouped(const void *x, int x_dtype, int64_t ldx, int64_t m,
+                                       const mambo_projection *proj, int count, int64_t blocks,
+                                       const mambo_gemm_config *cfg, uint8_t *xv, int64_t ldxv,
+                                       uint8_t *xs, int64_t ldxs, mambo_stream_t stream);
+
 /* The configuration mambo_iq3s_fp8_matmul uses when cfg == NULL. */
 int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out);
 

@@ -85,6 +85,8 @@ SIGNATURES = {
                                      ctypes.POINTER(GemmConfig), _vp]),
     "mambo_iq3s_fp8_matmul_grouped": (_i32, [_vp, _i64, _vp, _i64, _i64, ctypes.POINTER(Projection), _i32, _i64,
                                              ctypes.POINTER(GemmConfig), _vp]),
+    "mambo_iq3s_matmul_quantize_grouped": (_i32, [_vp, _i32, _i64, _i64, ctypes.POINTER(Projection), _i32, _i64,
+                                                  ctypes.POINTER(GemmConfig), _vp, _i64, _vp, _i64, _vp]),
     "mambo_gemm_default_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_gemm_check_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_gemm_config_enumerate": (_i64, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig), _i64]),

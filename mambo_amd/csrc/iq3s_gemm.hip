@@ -349,8 +349,11 @@ __device__ __forceinline__ void stream_tile_end(float (&acc)[U][4], float *red, 
 // [y*bps, y*bps + bps) for tokens [16z, 16z + 4U). Its W waves split each tile's blocks
 // (wave w takes blocks w, w + W, ...) and stream the tiles back to back through one
 // register ring, so the ring does not drain between tiles and the activations are
-// staged in LDS once per workgroup.
-template <int U, int W, bool kLdsAct>
+// staged in LDS once per workgroup. kQ != 0: xv holds unquantized rows (kQ = 1 bf16,
+// 2 f32; ldxv in elements) that the workgroup quantizes to MXFP8 into its LDS copy
+// itself (quantize_group32: the quantizer's arithmetic, so the codes are identical), in
+// place of a separate quantizer launch; xs is unused.
+template <int U, int W, bool kLdsAct, int kQ = 0>
 __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                              GroupArgs ga, int64_t ntiles, int tpw, int B, int bps,
@@ -379,11 +382,20 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     // the weights (HBM), which stay in flight across it.
     __shared__ uint32_t s_grid[512];
     const uint8_t *lut = reinterpret_cast<const uint8_t *>(s_grid);
+    static_assert(kQ == 0 || kLdsAct, "quantizing rows needs the LDS copy");
+    const int qgroups = rows * (K / 32); // kQ: 32-element groups to quantize
+    float qv[32];
     {
         const __amdgpu_buffer_rsrc_t gr = byte_rsrc(c_grid.fp8);
         for (int i = wave; i < 8; i += W)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (lds_ptr)(s_grid + 64 * i), 4, 4u * lane, 256u * i, 0, 0);
-        if constexpr (kLdsAct) {
+        if constexpr (kQ != 0) {
+            // the first group this thread quantizes: its loads go out before the ring's
+            // weight loads, so waiting for them leaves the weights in flight
+            if (tid < qgroups)
+                load_group32<kQ == 1>(xv, (m0 + tid / (K / 32)) * ldxv + 32 * (tid % (K / 32)), qv);
+        }
+        if constexpr (kLdsAct && kQ == 0) {
             // activation rows m0 .. m0+rows-1 as 16-byte chunks (K is a multiple of 256, so
             // none straddles rows), then their scales as dwords (K/32 is a multiple of 8;
             // the host stages only 4-byte aligned scale rows)
@@ -419,6 +431,20 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     __builtin_amdgcn_sched_barrier(0);
     if (tid < 20)
         reinterpret_cast<uint32_t *>(smem + L.zero)[tid] = tid < 16 ? 0u : 0x7F7F7F7Fu;
+    if constexpr (kQ != 0) {
+        // rows [m0, m0+rows) to E4M3 + E8M0 in the layout the staging copies produce
+        for (int gi = tid; gi < qgroups; gi += W * 64) {
+            const int r = gi / (K / 32), g = gi - r * (K / 32);
+            if (gi != tid)
+                load_group32<kQ == 1>(xv, (m0 + r) * ldxv + 32 * g, qv);
+            uint32_t codes[8];
+            const int e = quantize_group32(qv, codes);
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + L.x + r * K + 32 * g);
+            dst[0] = uint4{codes[0], codes[1], codes[2], codes[3]};
+            dst[1] = uint4{codes[4], codes[5], codes[6], codes[7]};
+            smem[L.xs + r * (K / 32) + g] = (uint8_t)(e + 127);
+        }
+    }
     // this wave's copies are done once at most the ring's kWLoads * (kDepth - 1) weight
     // loads are outstanding (s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and
     // lgkmcnt 11:8 left unconstrained)
@@ -1420,18 +1446,26 @@ struct StreamLaunch {
     int B, bps, atomic;
 };
 
-template <int U, int W, bool kLdsAct>
+template <int U, int W, bool kLdsAct, int kQ = 0>
 void launch_stream_uwa(const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
                        int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
-    hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs, ldxs,
-                       M, ga, sl.ntiles, sl.tpw, sl.B, sl.bps, sl.atomic);
+    hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct, kQ>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs,
+                       ldxs, M, ga, sl.ntiles, sl.tpw, sl.B, sl.bps, sl.atomic);
 }
 
+// quant: -1 for MXFP8 activations, else the MAMBO_DTYPE_* of unquantized rows that the
+// kernel quantizes itself (built for one 4-token sub-tile with LDS-staged rows only).
 template <int U, int W>
-void launch_stream_uw(bool lds_act, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                      const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
+void launch_stream_uw(bool lds_act, int quant, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv,
+                      int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
+    if constexpr (U == 1) {
+        if (quant == MAMBO_DTYPE_BF16)
+            return launch_stream_uwa<U, W, true, 1>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+        if (quant == MAMBO_DTYPE_F32)
+            return launch_stream_uwa<U, W, true, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+    }
     if (lds_act)
         launch_stream_uwa<U, W, true>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
     else
@@ -1442,12 +1476,12 @@ void launch_stream_uw(bool lds_act, const StreamLaunch &sl, hipStream_t stream, 
 constexpr int kStreamWaves[] = {1, 2, 4, 6, 8, 12, 16};
 
 template <int U>
-int launch_stream_u(int waves, bool lds_act, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv,
-                    int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
+int launch_stream_u(int waves, bool lds_act, int quant, const StreamLaunch &sl, hipStream_t stream,
+                    const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_stream_uw<U, WV>(lds_act, sl, stream, xv, ldxv, xs, ldxs, M, ga);                                     \
+        launch_stream_uw<U, WV>(lds_act, quant, sl, stream, xv, ldxv, xs, ldxs, M, ga);                              \
         break;
     switch (waves) {
         MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
@@ -1829,22 +1863,31 @@ extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blo
 
 namespace {
 
+// run_projections with quant >= 0 launched nothing: the configuration cannot quantize
+// the rows inside the GEMM.
+constexpr int kNotFused = 1;
+
+// quant: -1 when xv/xs are MXFP8 activations; else xv holds unquantized rows of dtype
+// quant (ldxv in elements, xs unused) for the stream kernel to quantize itself, and the
+// call returns kNotFused, launching nothing, when the configuration cannot do that.
 int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t m,
                     const mambo_projection *proj, int count, int64_t blocks, const mambo_gemm_config *cfg,
-                    hipStream_t s)
+                    hipStream_t s, int quant = -1)
 {
-    MAMBO_REQUIRE(xv && xs && proj, MAMBO_ERR_VALUE, "null pointer");
+    MAMBO_REQUIRE(xv && (xs || quant >= 0) && proj, MAMBO_ERR_VALUE, "null pointer");
     MAMBO_REQUIRE(count >= 1 && count <= kMaxGroup, MAMBO_ERR_VALUE, "count must be in [1, %d] (got %d)", kMaxGroup,
                   count);
     MAMBO_REQUIRE(m >= 1 && blocks >= 1, MAMBO_ERR_VALUE, "shape must be positive (M=%lld B=%lld)", (long long)m,
                   (long long)blocks);
     MAMBO_REQUIRE(blocks <= (1 << 20), MAMBO_ERR_VALUE, "K too large");
     const int64_t k = blocks * 256;
-    MAMBO_REQUIRE(ldxv >= k && ldxs >= k / 32, MAMBO_ERR_VALUE, "activation row strides must cover the row");
-    MAMBO_REQUIRE(ldxv < ((int64_t)1 << 27) && ldxs < ((int64_t)1 << 27), MAMBO_ERR_VALUE,
+    MAMBO_REQUIRE(ldxv >= k && (quant >= 0 || ldxs >= k / 32), MAMBO_ERR_VALUE,
+                  "activation row strides must cover the row");
+    MAMBO_REQUIRE(ldxv < ((int64_t)1 << 27) && (quant >= 0 || ldxs < ((int64_t)1 << 27)), MAMBO_ERR_VALUE,
                   "activation row stride too large");
-    MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
-                  "x_values base and row stride must be 16-byte aligned");
+    if (quant < 0)
+        MAMBO_REQUIRE((uintptr_t)xv % 16 == 0 && ldxv % 16 == 0, MAMBO_ERR_VALUE,
+                      "x_values base and row stride must be 16-byte aligned");
     GroupArgs ga = {};
     ga.count = count;
     int64_t tiles = 0, n_total = 0;
@@ -1880,6 +1923,14 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         rc = mambo_gemm_check_config(m, n_total, blocks, &c);
         if (rc)
             return rc;
+    }
+    if (quant >= 0) { // in-kernel quantization: stream kernel, one sub-tile, rows staged in LDS
+        const int64_t esz = quant == MAMBO_DTYPE_BF16 ? 2 : 4;
+        const int qrows = (int)std::min<int64_t>(4, m);
+        const int qlds = stream_lds(1, c.waves, qrows, (int)k, true).total;
+        if (c.kernel != MAMBO_GEMM_STREAM || m > 4 || (uintptr_t)xv % 16 != 0 || (ldxv * esz) % 16 != 0 ||
+            !stream_stages_act((int64_t)qrows * k * 33 / 32, qlds, c.waves) || qlds > kMaxDynLds)
+            return kNotFused;
     }
     const int bps = (int)cdiv(blocks, c.split_k);
     const int splits = (int)cdiv(blocks, bps);
@@ -1953,7 +2004,7 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         lds_act = stream_stages_act((int64_t)rows * k * 33 / 32,
                                     stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves);
         // the staging copies move activation scales as dwords
-        if ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0)
+        if (quant < 0 && ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0))
             lds_act = false;
         const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
         MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
@@ -1963,10 +2014,10 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic};
         sl.grid.x = (unsigned)cdiv(tiles, tpw);
         switch (U) {
-        case 1: rc = launch_stream_u<1>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        case 2: rc = launch_stream_u<2>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        case 3: rc = launch_stream_u<3>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        default: rc = launch_stream_u<4>(c.waves, lds_act, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        case 1: rc = launch_stream_u<1>(c.waves, lds_act, quant, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        case 2: rc = launch_stream_u<2>(c.waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        case 3: rc = launch_stream_u<3>(c.waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
+        default: rc = launch_stream_u<4>(c.waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
         }
     }
     if (rc)
@@ -1992,4 +2043,24 @@ extern "C" int mambo_iq3s_fp8_matmul_grouped(const uint8_t *xv, int64_t ldxv, co
                                              const mambo_gemm_config *cfg, mambo_stream_t stream)
 {
     return run_projections(xv, ldxv, xs, ldxs, m, proj, count, blocks, cfg, (hipStream_t)stream);
+}
+
+extern "C" int mambo_iq3s_matmul_quantize_grouped(const void *x, int x_dtype, int64_t ldx, int64_t m,
+                                                  const mambo_projection *proj, int count, int64_t blocks,
+                                                  const mambo_gemm_config *cfg, uint8_t *xv, int64_t ldxv,
+                                                  uint8_t *xs, int64_t ldxs, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(x_dtype == MAMBO_DTYPE_F32 || x_dtype == MAMBO_DTYPE_BF16, MAMBO_ERR_VALUE,
+                  "activation dtype must be float32 or bfloat16");
+    MAMBO_REQUIRE(x && xv && xs, MAMBO_ERR_VALUE, "null pointer");
+    MAMBO_REQUIRE(m >= 1 && blocks >= 1 && blocks <= (1 << 20), MAMBO_ERR_VALUE, "shape must be positive");
+    const hipStream_t s = (hipStream_t)stream;
+    const int rc = run_projections(reinterpret_cast<const uint8_t *>(x), ldx, nullptr, 0, m, proj, count, blocks, cfg,
+                                   s, x_dtype);
+    if (rc != kNotFused)
+        return rc;
+    const int qrc = mambo_quantize_mxfp8(x, x_dtype, m, blocks * 256, ldx, xv, ldxv, xs, ldxs, stream);
+    if (qrc)
+        return qrc;
+    return run_projections(xv, ldxv, xs, ldxs, m, proj, count, blocks, cfg, s);
 }

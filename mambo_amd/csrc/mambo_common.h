@@ -183,3 +183,69 @@ __device__ __forceinline__ uint32_t e4m3_rne_sw(float y)
     }
     return sign | code;
 }
+
+// E4M3 rounding path of the quantizer: hardware v_cvt_pk_fp8_f32 (true) or the integer
+// restatement e4m3_rne_sw (false). The two agree on every f32 with |x| <= 464 (checked
+// on gfx950 over all 2^31 such bit patterns with both signs); the quantizer only feeds
+// |x * 2^-e| <= 448.
+constexpr bool kQuantHwCvt = true;
+
+// One 32-element MXFP8 group of an unquantized row (bf16 or f32, 16-byte aligned):
+// load_group32 reads it as f32 values, quantize_group32 returns its exponent e (the
+// E8M0 scale byte is e + 127) and writes the 32 E4M3 codes of x * 2^-e, little-endian
+// four per word - the arithmetic of quantize_mxfp8_kernel, so the codes match it.
+template <bool kBf16>
+__device__ __forceinline__ void load_group32(const void *__restrict__ x, int64_t off, float (&v)[32])
+{
+    if constexpr (kBf16) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + off);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 w = p[i];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * i + 2 * j] = __uint_as_float(ws[j] << 16);
+                v[8 * i + 2 * j + 1] = __uint_as_float(ws[j] & 0xFFFF0000u);
+            }
+        }
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + off);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 f = p[i];
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+    }
+}
+
+// Four E4M3 codes packed little-endian.
+template <bool kHw>
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d)
+{
+    if constexpr (kHw) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+        return (uint32_t)w;
+    } else {
+        return e4m3_rne_sw(a) | (e4m3_rne_sw(b) << 8) | (e4m3_rne_sw(c) << 16) | (e4m3_rne_sw(d) << 24);
+    }
+}
+
+__device__ __forceinline__ int quantize_group32(const float (&v)[32], uint32_t (&codes)[8])
+{
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        amax = fmaxf(amax, fabsf(v[i]));
+    const int e = mxfp8_exponent(amax);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        codes[i] = pack4<kQuantHwCvt>(__builtin_ldexpf(v[4 * i], -e), __builtin_ldexpf(v[4 * i + 1], -e),
+                                      __builtin_ldexpf(v[4 * i + 2], -e), __builtin_ldexpf(v[4 * i + 3], -e));
+    return e;
+}
+

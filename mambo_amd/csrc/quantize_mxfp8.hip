@@ -14,11 +14,6 @@
 
 namespace {
 
-// E4M3 rounding path of the quantizer: hardware v_cvt_pk_fp8_f32 (true) or the integer
-// restatement e4m3_rne_sw (false). The two agree on every f32 with |x| <= 464 (checked
-// on gfx950 over all 2^31 such bit patterns with both signs); the quantizer only feeds
-// |x * 2^-e| <= 448.
-constexpr bool kQuantHwCvt = true;
 
 // Rows per workgroup iteration: the loads of both rows are issued before either is
 // converted, two 16-byte loads in flight per lane ([4096,4096] bf16: 4345 -> 4565 GB/s;
@@ -59,19 +54,6 @@ __device__ __forceinline__ void load8_scalar(const void *__restrict__ x, int64_t
             v[i] = __uint_as_float((uint32_t)(reinterpret_cast<const uint16_t *>(x)[off + i]) << 16);
         else
             v[i] = reinterpret_cast<const float *>(x)[off + i];
-    }
-}
-
-// Four E4M3 codes packed little-endian.
-template <bool kHw>
-__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d)
-{
-    if constexpr (kHw) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-        return (uint32_t)w;
-    } else {
-        return e4m3_rne_sw(a) | (e4m3_rne_sw(b) << 8) | (e4m3_rne_sw(c) << 16) | (e4m3_rne_sw(d) << 24);
     }
 }
 

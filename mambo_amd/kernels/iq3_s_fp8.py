@@ -244,6 +244,53 @@ def launch_iq3_s_fp8_matmul_grouped(x_values: torch.Tensor, x_scales: torch.Tens
     return result
 
 
+def launch_iq3_s_matmul_quantize(x: torch.Tensor, iq3_weights, *, stream=None, config: dict | None = None,
+                                 outs=None):
+    """MXFP8 quantization of ``x`` and the projection(s) in one call (no reference
+    counterpart: the reference runs launch_quantize_fp8 and then
+    launch_iq3_s_fp8_matmul, quantize_fp8.py:1-4). ``x``: float32 or bfloat16 [M, K] on
+    the GPU. ``iq3_weights``: one IQ3SFields (returns a tensor) or 1..4 with the same K
+    (returns a list, as launch_iq3_s_fp8_matmul_grouped). For M <= 4 on the stream
+    kernel every workgroup quantizes the rows into its LDS copy itself - one launch
+    instead of two, results bit-identical to the two-step path under the same config;
+    other shapes run the quantizer and the GEMM back to back on the stream."""
+    single = isinstance(iq3_weights, IQ3SFields)
+    weights = [iq3_weights] if single else list(iq3_weights)
+    if not 1 <= len(weights) <= _native.MAX_GROUP:
+        raise ValueError(f"between 1 and {_native.MAX_GROUP} weights per call")
+    dims = [_weight_dimensions(w) for w in weights]
+    k_blocks = dims[0][1]
+    if any(b != k_blocks for _, b in dims):
+        raise ValueError("weights must share K")
+    k = k_blocks * IQ3_S_BLOCK_VALUES
+    if not isinstance(x, torch.Tensor) or x.ndim != 2 or x.shape[0] < 1 or x.shape[1] != k:
+        raise ValueError(f"x must be [M,{k}]")
+    dtypes = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16}
+    if x.dtype not in dtypes:
+        raise ValueError(f"x must be float32 or bfloat16, got {x.dtype}")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    m, dev = int(x.shape[0]), x.device
+    if outs is not None and len(outs) != len(weights):
+        raise ValueError("outs must hold one output per weight")
+    n_total = sum(n for n, _ in dims)
+    with torch.cuda.device(dev):
+        cfg = _native.GemmConfig.from_dict(config if config is not None else select_config(m, n_total, k))
+        result = [_output(None if outs is None else outs[i], m, n, dev) for i, (n, _) in enumerate(dims)]
+        projections = (_native.Projection * len(weights))()
+        for i, (w, (n, _)) in enumerate(zip(weights, dims)):
+            projections[i] = _native.Projection(ensure_packed(w, stream).data_ptr(), n, result[i].data_ptr(),
+                                                result[i].stride(0))
+        # MXFP8 buffers for shapes that quantize in a launch of their own
+        xv = torch.empty((m, k), dtype=torch.uint8, device=dev)
+        xs = torch.empty((m, k // 32), dtype=torch.uint8, device=dev)
+        _native.check(_native.lib().mambo_iq3s_matmul_quantize_grouped(
+            x.data_ptr(), dtypes[x.dtype], x.stride(0), m, projections, len(weights), k_blocks, cfg,
+            xv.data_ptr(), xv.stride(0), xs.data_ptr(), xs.stride(0), _native.stream_handle(stream)),
+            "launch_iq3_s_matmul_quantize")
+    return result[0] if single else result
+
+
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     """Candidate launch configurations for the autotuner (the analogue of the cuTile
     search spaces of iq3_s_fp8.py:416-459), as mambo_gemm_config_enumerate lists them:

@@ -46,6 +46,12 @@ def test_status_codes_and_last_error():
         _native.check(rc)
     rc = lib.mambo_iq3s_prepare(None, 4, 1, 110, 110, 1, None, None, None, None, None, None, None)
     assert rc == _native.MAMBO_ERR_VALUE
+    # the quantize + matmul entry point validates dtype and pointers before device work
+    rc = lib.mambo_iq3s_matmul_quantize_grouped(None, 7, 256, 1, None, 1, 1, None, None, 256, None, 8, None)
+    assert rc == _native.MAMBO_ERR_VALUE and b"dtype" in lib.mambo_last_error()
+    rc = lib.mambo_iq3s_matmul_quantize_grouped(None, _native.DTYPE_BF16, 256, 1, None, 1, 1, None, None, 256, None,
+                                                8, None)
+    assert rc == _native.MAMBO_ERR_VALUE and b"null" in lib.mambo_last_error()
     assert lib.mambo_iq3s_packed_bytes(0, 3) == 0
     assert lib.mambo_iq3s_packed_bytes(17, 3) == 2 * 3 * 1760
     assert lib.mambo_iq3s_packed_bytes(4096, 16) == 4096 * 16 * 110  # byte-preserving
