@@ -1592,6 +1592,11 @@ constexpr int kMaxLdsAct = MAMBO_MAX_LDS_ACT_KB * 1024;
 constexpr int64_t kCUs = 256;
 // Workgroups the stream kernel's default aims for when it has many tiles.
 constexpr int64_t kStreamWgs = 512;
+// Most workgroups of a stream launch that quantizes its activations itself.
+#ifndef MAMBO_FUSED_WGS
+#define MAMBO_FUSED_WGS 1024
+#endif
+constexpr int64_t kFusedWgs = MAMBO_FUSED_WGS;
 // Token count from which the default configuration uses the tiled kernel.
 constexpr int64_t kTiledMinM = 64;
 // Dynamic LDS per workgroup (the static codebook tables add 2.3 KiB).
@@ -2010,7 +2015,12 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
                       "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
                       c.waves, (long long)m);
-        const int tpw = (int)std::min<int64_t>(c.tile_n ? c.tile_n / kTileRows : 1, tiles);
+        int64_t runs = c.tile_n ? c.tile_n / kTileRows : 1;
+        // quantizing inside the GEMM repeats the rows' quantization in every workgroup:
+        // longer runs keep the workgroup count (and that repeated work) bounded
+        if (quant >= 0)
+            runs = std::max<int64_t>(runs, cdiv(tiles, kFusedWgs));
+        const int tpw = (int)std::min<int64_t>(runs, tiles);
         StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic};
         sl.grid.x = (unsigned)cdiv(tiles, tpw);
         switch (U) {
