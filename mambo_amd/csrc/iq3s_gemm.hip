@@ -959,11 +959,13 @@ __device__ __forceinline__ void stage_block(uint8_t *buf, __amdgpu_buffer_rsrc_t
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xrows, (lds_ptr)(buf + 1024 * i), 16,
                                                  (uint32_t)min(row, last_row) * ldxv + 16u * c, 256u * b, 0, 0);
     }
-    constexpr int kSInst = kRows / 32;
+    constexpr int kSInst = (kRows + 31) / 32; // a 16-row tile copies its scales with half the lanes
     for (int i = wave; i < kSInst; i += W) {
         const int row = 32 * i + (lane >> 1);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(srows, (lds_ptr)(buf + TiledBlock<MT>::kValues + 256 * i), 4,
-                                                 (uint32_t)min(row, last_row) * ldxs + 4u * (lane & 1), 8u * b, 0, 0);
+        if (kRows >= 32 || lane < 2 * kRows)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(srows, (lds_ptr)(buf + TiledBlock<MT>::kValues + 256 * i), 4,
+                                                     (uint32_t)min(row, last_row) * ldxs + 4u * (lane & 1), 8u * b, 0,
+                                                     0);
     }
 }
 
@@ -1077,6 +1079,9 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
 {
     constexpr int kRows = TiledBlock<MT>::kRows;
     constexpr int kThreads = W * 64;
+    // a 16-token tile reads each weight once per launch: stream it (non-temporal), as the
+    // decode kernels do; larger token tiles re-read it once per token tile
+    constexpr int kPolicy = MT == 1 ? kStreamPolicy : 0;
     __shared__ __align__(16) uint8_t s_buf0[TiledBlock<MT>::kBytes];
     __shared__ __align__(16) uint8_t s_buf1[TiledBlock<MT>::kBytes];
     __shared__ uint32_t s_lvl[512];
@@ -1146,7 +1151,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     float d[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-        wcur[nt] = load_w_rsrc<0>(wt[nt], (uint32_t)b0 * kTileBytes, lane, col);
+        wcur[nt] = load_w_rsrc<kPolicy>(wt[nt], (uint32_t)b0 * kTileBytes, lane, col);
     stage_block<MT, W>(s_buf0, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, b0, wave, lane);
     __syncthreads();
 
@@ -1167,11 +1172,11 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
             mfma_half<MT, NT, 0>(cur, ao, soff, hh, hl, d, acc);                                                   \
             decode_half<NT, 1>(wcur, lvl, s_split, hh, hl);                                                        \
             for (int nt = 0; nt < NT; ++nt)                                                                        \
-                wcur[nt] = load_w_rsrc<0>(wt[nt], next_, lane, col);                                               \
+                wcur[nt] = load_w_rsrc<kPolicy>(wt[nt], next_, lane, col);                                         \
             mfma_half<MT, NT, 1>(cur, ao, soff, hh, hl, d, acc);                                                   \
         } else {                                                                                                   \
             for (int nt = 0; nt < NT; ++nt)                                                                        \
-                wnext[nt] = load_w_rsrc<0>(wt[nt], next_, lane, col);                                              \
+                wnext[nt] = load_w_rsrc<kPolicy>(wt[nt], next_, lane, col);                                        \
             __builtin_amdgcn_sched_barrier(0);                                                                     \
             decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);                                                       \
             mfma_block<MT, NT>(cur, ao, soff, bh, bl, d, acc);                                                     \
@@ -1568,6 +1573,7 @@ int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const
         launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                          \
         return MAMBO_OK;                                                                                           \
     }
+    MAMBO_T(1, 1, 4) MAMBO_T(1, 2, 4) MAMBO_T(1, 4, 4)
     MAMBO_T(16, 1, 16) MAMBO_T(16, 1, 8) MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
     MAMBO_T(4, 2, 8) MAMBO_T(4, 2, 4) MAMBO_T(4, 1, 8) MAMBO_T(4, 1, 4)
 #undef MAMBO_T
@@ -1766,9 +1772,17 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
     MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM || cfg->kernel == MAMBO_GEMM_DENSE ||
                       cfg->kernel == MAMBO_GEMM_TILED,
                   MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
+    if (cfg->kernel == MAMBO_GEMM_TILED && cfg->tile_m == 16) {
+        MAMBO_REQUIRE(cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128 || cfg->tile_n == 256),
+                      MAMBO_ERR_VALUE, "tiled: tile_m=16 is built for 4 waves of 16, 32 or 64 weight rows (tile_n=64, "
+                                       "128 or 256)");
+        MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
+                      "split_k must be in [1, K/256]");
+        return MAMBO_OK;
+    }
     if (cfg->kernel == MAMBO_GEMM_TILED) {
         MAMBO_REQUIRE(cfg->tile_m == 64 || cfg->tile_m == 128 || cfg->tile_m == 256, MAMBO_ERR_VALUE,
-                      "tiled: tile_m must be 64, 128 or 256");
+                      "tiled: tile_m must be 16, 64, 128 or 256");
         MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8 || (cfg->waves == 16 && cfg->tile_m == 256), MAMBO_ERR_VALUE,
                       "tiled: waves must be 4 or 8 (16 only with tile_m=256)");
         MAMBO_REQUIRE(cfg->tile_n == 16 * cfg->waves || cfg->tile_n == 32 * cfg->waves, MAMBO_ERR_VALUE,
@@ -1802,8 +1816,9 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
 // the stream kernel up to 16 tokens and the dense kernel up to 128 (both re-read every
 // weight once per 16- or 32-token chunk, so neither is a candidate beyond), each over
 // waves per workgroup x K split x weight rows (and, dense above 16 tokens, tokens) per
-// workgroup; from 32 tokens the tiled kernel's tile shapes x K split. Every entry but the
-// first passes mambo_gemm_check_config for the shape.
+// workgroup; for 5..64 tokens the tiled kernel's 16-token tiles and from 32 its larger
+// tile shapes, x K split. Every entry but the first passes mambo_gemm_check_config for
+// the shape.
 extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out,
                                                int64_t capacity)
 {
@@ -1850,6 +1865,11 @@ extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blo
             }
         }
     }
+    if (m > 4 && m <= 64) // 16-token tiles: four waves share each activation block through LDS
+        for (const int32_t rows : {16, 32, 64})
+            for (const int32_t split : {1, 2, 4})
+                if (split <= blocks)
+                    add(MAMBO_GEMM_TILED, 4, split, 16, rows * 4);
     if (m >= 32) { // tokens x weight rows per wave x waves
         for (const int32_t tile_m : {64, 128, 256})
             for (const int32_t waves : {4, 8, 16})

@@ -297,8 +297,8 @@ def gemm_search_space(m: int, n: int, k: int) -> list[dict]:
     led by the library default for the token count, then the block-diagonal stream kernel
     up to 16 tokens and the dense kernel up to 128 (each re-reads every weight once per
     16- or 32-token chunk, so neither is a candidate beyond), x waves per workgroup x K
-    split x weight rows (and, dense above 16 tokens, tokens) per workgroup; for M >= 32
-    the tiled kernel's tile shapes."""
+    split x weight rows (and, dense above 16 tokens, tokens) per workgroup; the tiled
+    kernel's 16-token tiles for 5..64 tokens and its larger tile shapes from 32."""
     if k % IQ3_S_BLOCK_VALUES:
         raise ValueError(f"K={k} must be a multiple of {IQ3_S_BLOCK_VALUES}")
     lib = _native.lib()

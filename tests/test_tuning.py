@@ -109,7 +109,8 @@ def test_tuned_table_round_trip_and_lookup(tmp_path, monkeypatch):
 
 def test_search_space_families_and_validity():
     """The library default leads every search space; stream candidates only up to 16
-    tokens, dense up to 128, tiled from 32; every candidate passes the library's own
+    tokens, dense up to 128, tiled from 5 (16-token tiles up to 64, larger ones from 32);
+    every candidate passes the library's own
     configuration check for its shape (no launches)."""
     import ctypes
 
@@ -123,7 +124,8 @@ def test_search_space_families_and_validity():
         kernels = {c["kernel"] for c in space[1:]}
         assert (_native.GEMM_STREAM in kernels) == (m <= 16), m
         assert (_native.GEMM_DENSE in kernels) == (m <= 128), m
-        assert (_native.GEMM_TILED in kernels) == (m >= 32), m
+        assert (_native.GEMM_TILED in kernels) == (m > 4), m
+        assert any(c["kernel"] == _native.GEMM_TILED and c["tile_m"] == 16 for c in space) == (4 < m <= 64), m
         assert len({tuple(sorted(c.items())) for c in space}) == len(space)
         for c in space:
             cfg = _native.GemmConfig.from_dict(c)
