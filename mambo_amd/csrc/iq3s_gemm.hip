@@ -1573,7 +1573,7 @@ int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const
         launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                          \
         return MAMBO_OK;                                                                                           \
     }
-    MAMBO_T(1, 1, 4) MAMBO_T(1, 2, 4) MAMBO_T(1, 4, 4)
+    MAMBO_T(1, 1, 4) MAMBO_T(1, 2, 4) MAMBO_T(1, 4, 4) MAMBO_T(2, 1, 4) MAMBO_T(2, 2, 4) MAMBO_T(2, 1, 8)
     MAMBO_T(16, 1, 16) MAMBO_T(16, 1, 8) MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
     MAMBO_T(4, 2, 8) MAMBO_T(4, 2, 4) MAMBO_T(4, 1, 8) MAMBO_T(4, 1, 4)
 #undef MAMBO_T
@@ -1772,17 +1772,23 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
     MAMBO_REQUIRE(cfg->kernel == MAMBO_GEMM_STREAM || cfg->kernel == MAMBO_GEMM_DENSE ||
                       cfg->kernel == MAMBO_GEMM_TILED,
                   MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
-    if (cfg->kernel == MAMBO_GEMM_TILED && cfg->tile_m == 16) {
-        MAMBO_REQUIRE(cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128 || cfg->tile_n == 256),
-                      MAMBO_ERR_VALUE, "tiled: tile_m=16 is built for 4 waves of 16, 32 or 64 weight rows (tile_n=64, "
-                                       "128 or 256)");
+    if (cfg->kernel == MAMBO_GEMM_TILED && (cfg->tile_m == 16 || cfg->tile_m == 32)) {
+        if (cfg->tile_m == 16)
+            MAMBO_REQUIRE(cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128 || cfg->tile_n == 256),
+                          MAMBO_ERR_VALUE, "tiled: tile_m=16 is built for 4 waves of 16, 32 or 64 weight rows (tile_n=64, "
+                                           "128 or 256)");
+        else
+            MAMBO_REQUIRE((cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128)) ||
+                              (cfg->waves == 8 && cfg->tile_n == 128),
+                          MAMBO_ERR_VALUE, "tiled: tile_m=32 is built for 4 waves of 16 or 32 weight rows (tile_n=64 "
+                                           "or 128) or 8 waves of 16 (tile_n=128)");
         MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                       "split_k must be in [1, K/256]");
         return MAMBO_OK;
     }
     if (cfg->kernel == MAMBO_GEMM_TILED) {
         MAMBO_REQUIRE(cfg->tile_m == 64 || cfg->tile_m == 128 || cfg->tile_m == 256, MAMBO_ERR_VALUE,
-                      "tiled: tile_m must be 16, 64, 128 or 256");
+                      "tiled: tile_m must be 16, 32, 64, 128 or 256");
         MAMBO_REQUIRE(cfg->waves == 4 || cfg->waves == 8 || (cfg->waves == 16 && cfg->tile_m == 256), MAMBO_ERR_VALUE,
                       "tiled: waves must be 4 or 8 (16 only with tile_m=256)");
         MAMBO_REQUIRE(cfg->tile_n == 16 * cfg->waves || cfg->tile_n == 32 * cfg->waves, MAMBO_ERR_VALUE,
@@ -1816,8 +1822,8 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
 // the stream kernel up to 16 tokens and the dense kernel up to 128 (both re-read every
 // weight once per 16- or 32-token chunk, so neither is a candidate beyond), each over
 // waves per workgroup x K split x weight rows (and, dense above 16 tokens, tokens) per
-// workgroup; for 5..64 tokens the tiled kernel's 16-token tiles and from 32 its larger
-// tile shapes, x K split. Every entry but the first passes mambo_gemm_check_config for
+// workgroup; for 5..64 tokens the tiled kernel's 16-token tiles (32-token ones from 17)
+// and from 32 its larger tile shapes, x K split. Every entry but the first passes mambo_gemm_check_config for
 // the shape.
 extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out,
                                                int64_t capacity)
@@ -1870,6 +1876,13 @@ extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blo
             for (const int32_t split : {1, 2, 4})
                 if (split <= blocks)
                     add(MAMBO_GEMM_TILED, 4, split, 16, rows * 4);
+    if (m > 16 && m <= 64) // 32-token tiles
+        for (const int32_t waves : {4, 8})
+            for (const int32_t rows : {16, 32})
+                if (waves == 4 || rows == 16)
+                    for (const int32_t split : {1, 2, 4})
+                        if (split <= blocks)
+                            add(MAMBO_GEMM_TILED, waves, split, 32, rows * waves);
     if (m >= 32) { // tokens x weight rows per wave x waves
         for (const int32_t tile_m : {64, 128, 256})
             for (const int32_t waves : {4, 8, 16})

@@ -126,6 +126,7 @@ def test_search_space_families_and_validity():
         assert (_native.GEMM_DENSE in kernels) == (m <= 128), m
         assert (_native.GEMM_TILED in kernels) == (m > 4), m
         assert any(c["kernel"] == _native.GEMM_TILED and c["tile_m"] == 16 for c in space) == (4 < m <= 64), m
+        assert any(c["kernel"] == _native.GEMM_TILED and c["tile_m"] == 32 for c in space) == (16 < m <= 64), m
         assert len({tuple(sorted(c.items())) for c in space}) == len(space)
         for c in space:
             cfg = _native.GemmConfig.from_dict(c)
