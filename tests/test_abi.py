@@ -105,11 +105,19 @@ def test_gemm_config_defaults_and_validation():
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_TILED, "split_k": 1, "tile_m": 256, **fields})
         assert lib.mambo_gemm_check_config(2048, 4096, 16, ctypes.byref(c)) == rc, fields
     # dense default: 32 tokens per workgroup above 16 tokens; tiles per workgroup by grid size
-    for m, n, tile_m, tile_n in ((16, 8192, 16, 32), (16, 57344, 16, 64), (32, 57344, 32, 64), (32, 8192, 32, 32),
-                                 (32, 10240, 32, 64), (24, 8192, 32, 32), (48, 57344, 32, 64)):
+    for m, n, tile_m, tile_n in ((16, 8192, 16, 32), (16, 57344, 16, 64), (48, 57344, 32, 64), (32, 1024, 32, 16)):
         c = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(m, n, 32, ctypes.byref(c)) == 0
         assert (c.kernel, c.tile_m, c.tile_n, c.waves) == (_native.GEMM_DENSE, tile_m, tile_n, 4), (m, n, c.as_dict())
+    # 17-32 tokens: 32-token tiles of 4 x 16 weight rows, K split toward ~512 workgroups
+    # (at most 4 splits of at least 8 blocks) unless the grid stays under half the CUs
+    for m, n, blocks, split in ((32, 57344, 32, 1), (32, 8192, 32, 4), (32, 10240, 32, 4), (24, 8192, 32, 4),
+                                (17, 28672, 16, 2), (32, 8192, 112, 4), (32, 4096, 16, 2)):
+        c = _native.GemmConfig()
+        assert lib.mambo_gemm_default_config(m, n, blocks, ctypes.byref(c)) == 0
+        assert (c.kernel, c.tile_m, c.tile_n, c.waves, c.split_k) == (_native.GEMM_TILED, 32, 64, 4, split), \
+            (m, n, blocks, c.as_dict())
+        assert lib.mambo_gemm_check_config(m, n, blocks, ctypes.byref(c)) == 0
     for fields, rc in (({"tile_m": 32, "waves": 4}, 0), ({"tile_m": 32, "waves": 16}, _native.MAMBO_ERR_VALUE),
                        ({"tile_m": 48, "waves": 4}, _native.MAMBO_ERR_VALUE)):
         c = _native.GemmConfig.from_dict({"kernel": _native.GEMM_DENSE, "split_k": 1, **fields})

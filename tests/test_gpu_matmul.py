@@ -360,3 +360,26 @@ def test_prefill_shape_sampled(gpu, n, k):
     expected = oracle.iq3s_fp8_matmul(xq.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
     check(out[:, rows], expected, elementwise=False)
     assert np.all(np.isfinite(out))
+
+
+def test_default_32_token_tiles(gpu):
+    """17-32 tokens on a wide enough grid: the library default is the tiled kernel's
+    32-token tile (four waves sharing each activation block) with K split."""
+    import ctypes
+
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n, k, m = 4096, 8192, 24
+    c = _native.GemmConfig()
+    assert _native.lib().mambo_gemm_default_config(m, n, k // 256, ctypes.byref(c)) == 0
+    assert (c.kernel, c.tile_m, c.split_k) == (_native.GEMM_TILED, 32, 4), c.as_dict()
+    raw = oracle.gen_iq3s(31, n, k // 256)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    x = np.random.default_rng(24).standard_normal((m, k)).astype(np.float32)
+    xv, xs = oracle.quantize_mxfp8(x)
+    step(f"default config M={m} N={n} K={k}: {c.as_dict()}")
+    out = launch_iq3_s_fp8_matmul(torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu), fields,
+                                  config={"kernel": _native.GEMM_AUTO})
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), oracle.iq3s_fp8_matmul(xv, xs, raw))
