@@ -1840,8 +1840,8 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
 // weight once per 16- or 32-token chunk, so neither is a candidate beyond), each over
 // waves per workgroup x K split x weight rows (and, dense above 16 tokens, tokens) per
 // workgroup; for 5..64 tokens the tiled kernel's 16-token tiles (32-token ones from 17)
-// and from 32 its larger tile shapes, x K split. Every entry but the first passes mambo_gemm_check_config for
-// the shape.
+// and from 32 its larger tile shapes, x K split. Every entry but the first passes
+// mambo_gemm_check_config for the shape.
 extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out,
                                                int64_t capacity)
 {
