@@ -59,18 +59,6 @@ struct WTile {
     uint16_t dh;  // fp16 d of row col
 };
 
-// tb is wave-uniform; the lane offsets are 32-bit so the loads use a scalar base.
-__device__ __forceinline__ WTile load_w(const uint8_t *__restrict__ tb, uint32_t lane, uint32_t col)
-{
-    WTile w;
-    w.ia = *reinterpret_cast<const uint4 *>(tb + (kTileIdxA + 16u * lane));
-    w.ib = *reinterpret_cast<const uint16_t *>(tb + (kTileIdxB + 2u * lane));
-    w.sg = *reinterpret_cast<const uint2 *>(tb + (kTileSigns + 8u * lane));
-    w.sc = tb[kTileScales + lane];
-    w.dh = *reinterpret_cast<const uint16_t *>(tb + (kTileD + 2u * col));
-    return w;
-}
-
 // Buffer resource over the 4 GiB that start at `base` (raw, unswizzled): loads through
 // it take a scalar base, a 32-bit lane offset, a scalar step offset and an immediate
 // field offset, with no per-lane 64-bit address arithmetic. The host keeps every offset
