@@ -181,3 +181,23 @@ def test_tuned_table_drops_shapes_the_default_won(tmp_path, monkeypatch):
         assert iq3_s_fp8.select_config(4, 8192, 8192, arch="gfx950") == iq3_s_fp8.default_config(4)
     finally:
         iq3_s_fp8._tuned_table.cache_clear()
+
+
+def test_committed_tuned_table_entries_are_valid():
+    """Every configuration of the committed gfx950 table passes the library's own check
+    for its shape (key N x K @ M bucket; no launches)."""
+    import ctypes
+    import json
+
+    from mambo_amd import _native
+    from mambo_amd.kernels import iq3_s_fp8
+    table = json.loads(iq3_s_fp8.TUNED_PATH.read_text())["gfx950"]
+    assert table
+    lib = _native.lib()
+    for key, cfg in table.items():
+        shape, m = key.split("@")
+        n, k = (int(v) for v in shape.split("x"))
+        c = _native.GemmConfig.from_dict(cfg)
+        assert c.kernel in (_native.GEMM_STREAM, _native.GEMM_DENSE, _native.GEMM_TILED), key
+        for tokens in (int(m) // 2 + 1, int(m)):  # both ends of the bucket
+            assert lib.mambo_gemm_check_config(tokens, n, k // 256, ctypes.byref(c)) == 0, (key, tokens, cfg)
