@@ -90,7 +90,7 @@ extern "C" int mambo_copy_bytes(const void *src, void *dst, int64_t bytes, mambo
                   "src and dst must be non-NULL and 16-byte aligned");
     const int64_t n16 = bytes / 16;
     const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 4096);
-    hipLaunchKernelGGL(copy_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+    MAMBO_LAUNCH(copy_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (const uint4 *)src, (uint4 *)dst, n16);
     return mambo_check_launch("copy_bytes");
 }
@@ -120,7 +120,7 @@ extern "C" int mambo_read_bytes(const void *src, int64_t bytes, uint32_t *sink, 
     MAMBO_REQUIRE(sink != nullptr, MAMBO_ERR_VALUE, "sink must not be NULL");
     MAMBO_REQUIRE(bytes == 0 || (src != nullptr && (uintptr_t)src % 16 == 0), MAMBO_ERR_VALUE,
                   "src must be non-NULL and 16-byte aligned");
-    hipLaunchKernelGGL(read_bytes_kernel, dim3((unsigned)kReadWorkgroups), dim3(256), 0, (hipStream_t)stream,
+    MAMBO_LAUNCH(read_bytes_kernel, dim3((unsigned)kReadWorkgroups), dim3(256), 0, (hipStream_t)stream,
                        (const uint4 *)src, bytes / 16, sink);
     return mambo_check_launch("read_bytes");
 }
@@ -153,7 +153,7 @@ extern "C" int mambo_mfma_peak(int64_t workgroups, int iters, float *out, mambo_
     MAMBO_REQUIRE(workgroups >= 1 && workgroups <= 65536, MAMBO_ERR_VALUE, "workgroups must be in [1, 65536]");
     MAMBO_REQUIRE(iters >= 0 && iters <= (1 << 20), MAMBO_ERR_VALUE, "iters must be in [0, 2^20]");
     MAMBO_REQUIRE(out != nullptr, MAMBO_ERR_VALUE, "out must not be NULL");
-    hipLaunchKernelGGL(mfma_peak_kernel, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
+    MAMBO_LAUNCH(mfma_peak_kernel, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
     return mambo_check_launch("mfma_peak");
 }
 
@@ -165,6 +165,6 @@ extern "C" int mambo_fill_f32(float *ptr, int64_t n, float value, mambo_stream_t
     MAMBO_REQUIRE(ptr != nullptr, MAMBO_ERR_VALUE, "ptr must not be NULL");
     int64_t blocks = (n + 1023) / 1024;
     MAMBO_REQUIRE(blocks <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "n too large");
-    hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, ptr, n, value);
+    MAMBO_LAUNCH(fill_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, ptr, n, value);
     return mambo_check_launch("fill_f32");
 }

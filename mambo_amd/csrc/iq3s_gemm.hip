@@ -26,6 +26,8 @@
 // partial dot product of exactly the group lane l decoded, so each lane post-scales its
 // own accumulator by its own group's F; the four g' partials are summed at the end.
 // M up to 4 per MFMA, up to 16 per pass (U = 1..4 MFMAs per K step).
+#include <functional>
+
 #include "mambo_common.h"
 
 namespace {
@@ -427,11 +429,11 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
             if (gi != tid)
                 load_group32<kQ == 1>(xv, (m0 + r) * ldxv + 32 * g, qv);
             uint32_t codes[8];
-            const int e = quantize_group32(qv, codes);
+            const int scale = quantize_group32(qv, codes);
             uint4 *dst = reinterpret_cast<uint4 *>(smem + L.x + r * K + 32 * g);
             dst[0] = uint4{codes[0], codes[1], codes[2], codes[3]};
             dst[1] = uint4{codes[4], codes[5], codes[6], codes[7]};
-            smem[L.xs + r * (K / 32) + g] = (uint8_t)(e + 127);
+            smem[L.xs + r * (K / 32) + g] = (uint8_t)scale;
         }
     }
     // this wave's copies are done once at most the ring's kWLoads * (kDepth - 1) weight
@@ -1444,7 +1446,7 @@ template <int U, int W, bool kLdsAct, int kQ = 0>
 void launch_stream_uwa(const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
                        int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
-    hipLaunchKernelGGL((gemm_stream_kernel<U, W, kLdsAct, kQ>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs,
+    MAMBO_LAUNCH((gemm_stream_kernel<U, W, kLdsAct, kQ>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs,
                        ldxs, M, ga, sl.ntiles, sl.tpw, sl.B, sl.bps, sl.atomic);
 }
 
@@ -1469,13 +1471,15 @@ void launch_stream_uw(bool lds_act, int quant, const StreamLaunch &sl, hipStream
 // Waves per workgroup the stream kernel is built for.
 constexpr int kStreamWaves[] = {1, 2, 4, 6, 8, 12, 16};
 
+// dry: check that the configuration is built, launch nothing.
 template <int U>
-int launch_stream_u(int waves, bool lds_act, int quant, const StreamLaunch &sl, hipStream_t stream,
+int launch_stream_u(bool dry, int waves, bool lds_act, int quant, const StreamLaunch &sl, hipStream_t stream,
                     const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_stream_uw<U, WV>(lds_act, quant, sl, stream, xv, ldxv, xs, ldxs, M, ga);                              \
+        if (!dry)                                                                                                  \
+            launch_stream_uw<U, WV>(lds_act, quant, sl, stream, xv, ldxv, xs, ldxs, M, ga);                          \
         break;
     switch (waves) {
         MAMBO_W(1) MAMBO_W(2) MAMBO_W(4) MAMBO_W(6) MAMBO_W(8) MAMBO_W(12) MAMBO_W(16)
@@ -1491,25 +1495,27 @@ void launch_dense_wnm(bool lds_act, dim3 grid, size_t lds, hipStream_t stream, c
                       const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     if (lds_act)
-        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, true, MC>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs,
+        MAMBO_LAUNCH((gemm_dense_kernel<W, NT, true, MC>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs,
                            M, ga, B, bps, atomic);
     else
-        hipLaunchKernelGGL((gemm_dense_kernel<W, NT, false, MC>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs,
+        MAMBO_LAUNCH((gemm_dense_kernel<W, NT, false, MC>), grid, dim3(W * 64), lds, stream, xv, ldxv, xs, ldxs,
                            M, ga, B, bps, atomic);
 }
 
 template <int NT>
-int launch_dense_n(int waves, int mc, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
-                   int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
-                   int atomic)
+int launch_dense_n(bool dry, int waves, int mc, bool lds_act, dim3 grid, size_t lds, hipStream_t stream,
+                   const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga,
+                   int B, int bps, int atomic)
 {
 #define MAMBO_W(WV)                                                                                                \
     case WV:                                                                                                       \
-        launch_dense_wnm<WV, NT, 1>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);         \
+        if (!dry)                                                                                                  \
+            launch_dense_wnm<WV, NT, 1>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);     \
         break;
 #define MAMBO_W2(WV)                                                                                               \
     case WV:                                                                                                       \
-        launch_dense_wnm<WV, NT, 2>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);         \
+        if (!dry)                                                                                                  \
+            launch_dense_wnm<WV, NT, 2>(lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);     \
         break;
     if (mc == 2) {
         switch (waves) {
@@ -1529,14 +1535,14 @@ int launch_dense_n(int waves, int mc, bool lds_act, dim3 grid, size_t lds, hipSt
     return MAMBO_OK;
 }
 
-int launch_dense(int waves, int nt, int mc, bool lds_act, dim3 grid, size_t lds, hipStream_t stream, const uint8_t *xv,
-                 int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
-                 int atomic)
+int launch_dense(bool dry, int waves, int nt, int mc, bool lds_act, dim3 grid, size_t lds, hipStream_t stream,
+                 const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B,
+                 int bps, int atomic)
 {
     switch (nt) {
-    case 1: return launch_dense_n<1>(waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
-    case 2: return launch_dense_n<2>(waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
-    case 4: return launch_dense_n<4>(waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 1: return launch_dense_n<1>(dry, waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 2: return launch_dense_n<2>(dry, waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
+    case 4: return launch_dense_n<4>(dry, waves, mc, lds_act, grid, lds, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);
     default: return mambo_fail(MAMBO_ERR_VALUE, "dense kernel: tile_n must be 16, 32 or 64 (got %d)", 16 * nt);
     }
 }
@@ -1546,20 +1552,21 @@ void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ld
                     int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
     if constexpr (MT >= 16 && W <= 8) // 256 x 128 x 8: register staging
-        hipLaunchKernelGGL((gemm_tiled_regs_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv,
+        MAMBO_LAUNCH((gemm_tiled_regs_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv,
                            ldxv, xs, ldxs, M, ga, B, bps, atomic);
     else // direct copies; 256 x 256 x 16 in the half-K form
-        hipLaunchKernelGGL((gemm_tiled_kernel<MT, NT, W, (MT >= 16)>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs,
+        MAMBO_LAUNCH((gemm_tiled_kernel<MT, NT, W, (MT >= 16)>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs,
                            ldxs, M, ga, B, bps, atomic);
 }
 
 // Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves).
-int launch_tiled(int mt, int nt, int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
+int launch_tiled(bool dry, int mt, int nt, int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
                  const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
 #define MAMBO_T(A, C, D)                                                                                           \
     if (mt == A && nt == C && waves == D) {                                                                        \
-        launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                          \
+        if (!dry)                                                                                                  \
+            launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                      \
         return MAMBO_OK;                                                                                           \
     }
     MAMBO_T(1, 1, 4) MAMBO_T(1, 2, 4) MAMBO_T(1, 4, 4) MAMBO_T(2, 1, 4) MAMBO_T(2, 2, 4) MAMBO_T(2, 1, 8)
@@ -1911,6 +1918,81 @@ namespace {
 // the rows inside the GEMM.
 constexpr int kNotFused = 1;
 
+// Checks and launch closure of the two streaming families (stream, dense) for
+// run_projections.
+int plan_streaming(const mambo_gemm_config &c, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
+                   int64_t m, const GroupArgs &ga, int64_t tiles, int64_t blocks, int64_t k, int bps, int splits,
+                   int atomic, int quant, hipStream_t s, std::function<int(bool)> &launch)
+{
+    const int64_t mchunks = cdiv(m, 16);
+    MAMBO_REQUIRE(tiles <= 0x7FFFFFFF && mchunks <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
+    const int rows = (int)std::min<int64_t>(16, m); // rows of the largest M chunk
+    // Stage the activations in LDS when they are small enough; otherwise read them from
+    // global memory (L2) in the weight ring.
+    bool lds_act = (int64_t)rows * k * 33 / 32 <= kMaxLdsAct;
+    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
+    const int B = (int)blocks;
+    if (c.kernel == MAMBO_GEMM_DENSE) {
+        const int nt = c.tile_n ? c.tile_n / kTileRows : 1;
+        const int mc = c.tile_m == 32 ? 2 : 1; // 16-token chunks per workgroup
+        const int drows = (int)std::min<int64_t>(16 * mc, m);
+        // workgroups per projection (NT tiles each); tile_begin counts workgroups
+        GroupArgs gd = ga;
+        int64_t wgs = 0;
+        for (int g = 0; g < ga.count; ++g) {
+            gd.tile_begin[g] = wgs;
+            wgs += cdiv(cdiv(ga.n[g], kTileRows), nt);
+        }
+        grid.x = (unsigned)wgs;
+        grid.z = (unsigned)cdiv(m, 16 * mc);
+        lds_act = (int64_t)drows * k * 33 / 32 <= kMaxLdsAct;
+        if ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0) // the staging copies move scales as dwords
+            lds_act = false;
+        if (lds_act && dense_lds(c.waves, nt, mc, drows, (int)k, true).total > kMaxDynLds)
+            lds_act = false;
+        const DenseLds L = dense_lds(c.waves, nt, mc, drows, (int)k, lds_act);
+        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
+                      "configuration needs %d bytes of LDS per workgroup (waves=%d, tile_n=%d, tile_m=%d)", L.total,
+                      c.waves, c.tile_n, c.tile_m);
+        const int waves = c.waves;
+        launch = [=](bool dry) {
+            return launch_dense(dry, waves, nt, mc, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, gd, B, bps,
+                                atomic);
+        };
+        return MAMBO_OK;
+    } else {
+        const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
+        lds_act = stream_stages_act((int64_t)rows * k * 33 / 32,
+                                    stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves);
+        // the staging copies move activation scales as dwords
+        if (quant < 0 && ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0))
+            lds_act = false;
+        const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
+        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
+                      "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
+                      c.waves, (long long)m);
+        int64_t runs = c.tile_n ? c.tile_n / kTileRows : 1;
+        // quantizing inside the GEMM repeats the rows' quantization in every workgroup:
+        // longer runs keep the workgroup count (and that repeated work) bounded
+        if (quant >= 0)
+            runs = std::max<int64_t>(runs, cdiv(tiles, kFusedWgs));
+        const int tpw = (int)std::min<int64_t>(runs, tiles);
+        StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic};
+        sl.grid.x = (unsigned)cdiv(tiles, tpw);
+        const int waves = c.waves;
+        launch = [=](bool dry) {
+            switch (U) {
+            case 1: return launch_stream_u<1>(dry, waves, lds_act, quant, sl, s, xv, ldxv, xs, ldxs, m, ga);
+            case 2: return launch_stream_u<2>(dry, waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga);
+            case 3: return launch_stream_u<3>(dry, waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga);
+            default: return launch_stream_u<4>(dry, waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga);
+            }
+        };
+        return MAMBO_OK;
+    }
+}
+
+
 // quant: -1 when xv/xs are MXFP8 activations; else xv holds unquantized rows of dtype
 // quant (ldxv in elements, xs unused) for the stream kernel to quantize itself, and the
 // call returns kNotFused, launching nothing, when the configuration cannot do that.
@@ -1979,17 +2061,13 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     const int bps = (int)cdiv(blocks, c.split_k);
     const int splits = (int)cdiv(blocks, bps);
     const int atomic = splits > 1;
-    if (atomic) {
+    if (atomic)
         MAMBO_REQUIRE(m <= 65535, MAMBO_ERR_VALUE, "M too large for split-K");
-        int64_t n_max = 0;
-        for (int g = 0; g < count; ++g)
-            n_max = std::max(n_max, ga.n[g]);
-        dim3 zg((unsigned)std::min<int64_t>(cdiv(n_max, 256), 1024), (unsigned)m, (unsigned)count);
-        hipLaunchKernelGGL(zero_rows_kernel, zg, dim3(256), 0, s, ga);
-        rc = mambo_check_launch("zero_rows");
-        if (rc)
-            return rc;
-    }
+    // The launch of the chosen family: dry = true checks that it is built, launching
+    // nothing. Every check runs before the K split's zero fill is queued, so a rejected
+    // call leaves the outputs and the stream untouched.
+    std::function<int(bool)> launch;
+    const char *what = "iq3s_fp8_matmul";
     if (c.kernel == MAMBO_GEMM_TILED) {
         const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);
         MAMBO_REQUIRE((uintptr_t)xs % 8 == 0 && ldxs % 8 == 0, MAMBO_ERR_VALUE,
@@ -2006,72 +2084,33 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         }
         const int64_t mtiles = cdiv(m, c.tile_m);
         MAMBO_REQUIRE(wgs <= 0x7FFFFFFF && mtiles <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
-        rc = launch_tiled(mt, nt, c.waves, dim3((unsigned)wgs, (unsigned)mtiles, (unsigned)splits), s, xv, ldxv, xs,
-                          ldxs, m, gt, (int)blocks, bps, atomic);
+        const dim3 grid((unsigned)wgs, (unsigned)mtiles, (unsigned)splits);
+        launch = [=](bool dry) {
+            return launch_tiled(dry, mt, nt, c.waves, grid, s, xv, ldxv, xs, ldxs, m, gt, (int)blocks, bps, atomic);
+        };
+        what = "iq3s_fp8_matmul (tiled)";
+    } else {
+        rc = plan_streaming(c, xv, ldxv, xs, ldxs, m, ga, tiles, blocks, k, bps, splits, atomic, quant, s, launch);
         if (rc)
             return rc;
-        return mambo_check_launch("iq3s_fp8_matmul (tiled)");
     }
-    const int64_t mchunks = cdiv(m, 16);
-    MAMBO_REQUIRE(tiles <= 0x7FFFFFFF && mchunks <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
-    const int rows = (int)std::min<int64_t>(16, m); // rows of the largest M chunk
-    // Stage the activations in LDS when they are small enough; otherwise read them from
-    // global memory (L2) in the weight ring.
-    bool lds_act = (int64_t)rows * k * 33 / 32 <= kMaxLdsAct;
-    dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)mchunks);
-    const int B = (int)blocks;
-    if (c.kernel == MAMBO_GEMM_DENSE) {
-        const int nt = c.tile_n ? c.tile_n / kTileRows : 1;
-        const int mc = c.tile_m == 32 ? 2 : 1; // 16-token chunks per workgroup
-        const int drows = (int)std::min<int64_t>(16 * mc, m);
-        // workgroups per projection (NT tiles each); tile_begin counts workgroups
-        GroupArgs gd = ga;
-        int64_t wgs = 0;
-        for (int g = 0; g < count; ++g) {
-            gd.tile_begin[g] = wgs;
-            wgs += cdiv(cdiv(ga.n[g], kTileRows), nt);
-        }
-        grid.x = (unsigned)wgs;
-        grid.z = (unsigned)cdiv(m, 16 * mc);
-        lds_act = (int64_t)drows * k * 33 / 32 <= kMaxLdsAct;
-        if ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0) // the staging copies move scales as dwords
-            lds_act = false;
-        if (lds_act && dense_lds(c.waves, nt, mc, drows, (int)k, true).total > kMaxDynLds)
-            lds_act = false;
-        const DenseLds L = dense_lds(c.waves, nt, mc, drows, (int)k, lds_act);
-        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
-                      "configuration needs %d bytes of LDS per workgroup (waves=%d, tile_n=%d, tile_m=%d)", L.total,
-                      c.waves, c.tile_n, c.tile_m);
-        rc = launch_dense(c.waves, nt, mc, lds_act, grid, L.total, s, xv, ldxv, xs, ldxs, m, gd, B, bps, atomic);
-    } else {
-        const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
-        lds_act = stream_stages_act((int64_t)rows * k * 33 / 32,
-                                    stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves);
-        // the staging copies move activation scales as dwords
-        if (quant < 0 && ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0))
-            lds_act = false;
-        const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
-        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
-                      "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
-                      c.waves, (long long)m);
-        int64_t runs = c.tile_n ? c.tile_n / kTileRows : 1;
-        // quantizing inside the GEMM repeats the rows' quantization in every workgroup:
-        // longer runs keep the workgroup count (and that repeated work) bounded
-        if (quant >= 0)
-            runs = std::max<int64_t>(runs, cdiv(tiles, kFusedWgs));
-        const int tpw = (int)std::min<int64_t>(runs, tiles);
-        StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic};
-        sl.grid.x = (unsigned)cdiv(tiles, tpw);
-        switch (U) {
-        case 1: rc = launch_stream_u<1>(c.waves, lds_act, quant, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        case 2: rc = launch_stream_u<2>(c.waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        case 3: rc = launch_stream_u<3>(c.waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        default: rc = launch_stream_u<4>(c.waves, lds_act, -1, sl, s, xv, ldxv, xs, ldxs, m, ga); break;
-        }
-    }
+    rc = launch(true);
     if (rc)
         return rc;
-    return mambo_check_launch("iq3s_fp8_matmul");
+    if (atomic) {
+        int64_t n_max = 0;
+        for (int g = 0; g < count; ++g)
+            n_max = std::max(n_max, ga.n[g]);
+        dim3 zg((unsigned)std::min<int64_t>(cdiv(n_max, 256), 1024), (unsigned)m, (unsigned)count);
+        MAMBO_LAUNCH(zero_rows_kernel, zg, dim3(256), 0, s, ga);
+        rc = mambo_check_launch("zero_rows");
+        if (rc)
+            return rc;
+    }
+    rc = launch(false);
+    if (rc)
+        return rc;
+    return mambo_check_launch(what);
 }
 
 } // namespace

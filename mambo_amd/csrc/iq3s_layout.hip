@@ -219,7 +219,7 @@ static int launch_prepare(const Src &src, int64_t n, int64_t blocks, uint16_t *d
     const int64_t tiles = (n + kTileRows - 1) / kTileRows;
     MAMBO_REQUIRE(tiles <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "N too large");
     dim3 grid((unsigned)tiles, (unsigned)(blocks < 65535 ? blocks : 65535));
-    hipLaunchKernelGGL(prepare_kernel<Src>, grid, dim3(256), 0, stream, src, n, blocks, d, qs, qh, signs, scales,
+    MAMBO_LAUNCH(prepare_kernel<Src>, grid, dim3(256), 0, stream, src, n, blocks, d, qs, qh, signs, scales,
                        packed);
     return mambo_check_launch("iq3s_prepare");
 }
@@ -260,7 +260,7 @@ extern "C" int mambo_iq3s_dequant(const uint16_t *d, const uint32_t *qs, const u
     MAMBO_REQUIRE((uintptr_t)values % 16 == 0, MAMBO_ERR_VALUE, "values must be 16-byte aligned");
     const int64_t total = n * blocks * 8;
     MAMBO_REQUIRE((total + 255) / 256 <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "weight too large");
-    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, d,
+    MAMBO_LAUNCH(dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, d,
                        qs, qh, signs, scales, n, blocks, values, out_scales);
     return mambo_check_launch("iq3s_dequant");
 }

@@ -11,6 +11,15 @@
 int mambo_fail(int status, const char *fmt, ...);
 int mambo_check_launch(const char *what);
 
+// Launch with the calling thread's HIP error state cleared first, so that the
+// mambo_check_launch after it reports this launch's own failure, not one that an
+// earlier, unrelated HIP call left behind.
+#define MAMBO_LAUNCH(...)                                                                          \
+    do {                                                                                           \
+        (void)hipGetLastError();                                                                   \
+        hipLaunchKernelGGL(__VA_ARGS__);                                                           \
+    } while (0)
+
 #define MAMBO_REQUIRE(cond, status, ...)                                                           \
     do {                                                                                           \
         if (!(cond))                                                                               \
@@ -235,17 +244,41 @@ __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d)
     }
 }
 
+// Non-finite inputs (outside the reference's tests: its numpy encoder raises on them and
+// its C++ tool rejects them). amax is taken over the magnitude bit patterns as unsigned
+// integers, so a NaN beats an infinity and an infinity beats every finite value. A group
+// whose amax is not finite gets the E8M0 NaN scale byte 0xFF (the whole group decodes to
+// NaN), and each of its codes is the E4M3 NaN 0x7F with the sign of its input.
+constexpr uint32_t kNonFiniteBits = 0x7F800000u;
+constexpr int kScaleNaN = 0xFF;
+
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+
+// Four E4M3 NaN codes carrying the signs of a..d.
+__device__ __forceinline__ uint32_t nan4(float a, float b, float c, float d)
+{
+    return 0x7F7F7F7Fu | ((__float_as_uint(a) >> 24) & 0x80u) | ((__float_as_uint(b) >> 16) & 0x8000u) |
+           ((__float_as_uint(c) >> 8) & 0x800000u) | (__float_as_uint(d) & 0x80000000u);
+}
+
+// Returns the E8M0 scale byte (e + 127, or kScaleNaN).
 __device__ __forceinline__ int quantize_group32(const float (&v)[32], uint32_t (&codes)[8])
 {
-    float amax = 0.0f;
+    uint32_t amax = 0u;
 #pragma unroll
     for (int i = 0; i < 32; ++i)
-        amax = fmaxf(amax, fabsf(v[i]));
-    const int e = mxfp8_exponent(amax);
+        amax = max(amax, abs_bits(v[i]));
+    if (amax >= kNonFiniteBits) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            codes[i] = nan4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        return kScaleNaN;
+    }
+    const int e = mxfp8_exponent(__uint_as_float(amax));
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         codes[i] = pack4<kQuantHwCvt>(__builtin_ldexpf(v[4 * i], -e), __builtin_ldexpf(v[4 * i + 1], -e),
                                       __builtin_ldexpf(v[4 * i + 2], -e), __builtin_ldexpf(v[4 * i + 3], -e));
-    return e;
+    return e + 127;
 }
 

@@ -4,7 +4,8 @@
 // (src/python/mambo/kernels/quantize_fp8.py:23-52): per 32 consecutive K elements of a
 // row, amax -> e = max(ceil(log2(amax/448)), -127) (e = 0 when amax == 0), one E8M0
 // scale byte e+127 and 32 E4M3 codes of x * 2^-e rounded to nearest even. The exponent
-// is computed exactly from the bits of amax instead of through f32 log2.
+// is computed exactly from the bits of amax instead of through f32 log2. A group holding
+// a NaN or an infinity gets scale byte 0xFF and E4M3 NaN codes (quantize_group32).
 //
 // Mapping: four lanes per 32-element group, eight elements per lane, so every
 // wave-wide load and store instruction covers one contiguous span (bf16: 1 KiB per
@@ -86,21 +87,28 @@ __global__ __launch_bounds__(256) void quantize_mxfp8_kernel(const void *__restr
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int64_t row = row0 + r;
-            float amax = 0.0f;
+            // amax over the magnitude bit patterns (NaN > inf > finite; see quantize_group32)
+            uint32_t amax = 0u;
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                amax = fmaxf(amax, fabsf(v[r][i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1));
-            amax = fmaxf(amax, __shfl_xor(amax, 2));
-            const int e = mxfp8_exponent(amax);
+                amax = max(amax, abs_bits(v[r][i]));
+            amax = max(amax, (uint32_t)__shfl_xor((int)amax, 1));
+            amax = max(amax, (uint32_t)__shfl_xor((int)amax, 2));
+            const bool finite = amax < kNonFiniteBits;
+            const int e = finite ? mxfp8_exponent(__uint_as_float(amax)) : 0;
             if (ok && row < m) {
                 float y[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     y[i] = __builtin_ldexpf(v[r][i], -e); // exact scaling by a power of two
                 uint2 out;
-                out.x = pack4<kHw>(y[0], y[1], y[2], y[3]);
-                out.y = pack4<kHw>(y[4], y[5], y[6], y[7]);
+                if (finite) {
+                    out.x = pack4<kHw>(y[0], y[1], y[2], y[3]);
+                    out.y = pack4<kHw>(y[4], y[5], y[6], y[7]);
+                } else {
+                    out.x = nan4(y[0], y[1], y[2], y[3]);
+                    out.y = nan4(y[4], y[5], y[6], y[7]);
+                }
                 uint8_t *vp = values + row * ldv + 32 * g + 8 * j;
                 if constexpr (kVec) {
                     __builtin_nontemporal_store(u32x2{out.x, out.y}, reinterpret_cast<u32x2 *>(vp));
@@ -112,7 +120,7 @@ __global__ __launch_bounds__(256) void quantize_mxfp8_kernel(const void *__restr
                     }
                 }
                 if (j == 0)
-                    scales[row * lds + g] = (uint8_t)(e + 127);
+                    scales[row * lds + g] = (uint8_t)(finite ? e + 127 : kScaleNaN);
             }
         }
     }
@@ -137,7 +145,7 @@ int launch(const void *x, int64_t m, int64_t groups, int64_t ldx, uint8_t *value
 {
     const int64_t ry = (m + kQuantRows - 1) / kQuantRows;
     dim3 grid((unsigned)((groups + 63) / 64), (unsigned)(ry < 65535 ? ry : 65535));
-    hipLaunchKernelGGL((quantize_mxfp8_kernel<kBf16, kVec, kQuantHwCvt>), grid, dim3(256), 0, stream,
+    MAMBO_LAUNCH((quantize_mxfp8_kernel<kBf16, kVec, kQuantHwCvt>), grid, dim3(256), 0, stream,
                        x, ldx, m, groups, values, ldv, scales, lds);
     return mambo_check_launch("quantize_mxfp8");
 }
@@ -174,7 +182,7 @@ extern "C" int mambo_e4m3_convert(const float *in, int64_t n, uint8_t *out_sw, u
     MAMBO_REQUIRE(n >= 0 && in != nullptr, MAMBO_ERR_VALUE, "bad input");
     if (n == 0)
         return MAMBO_OK;
-    hipLaunchKernelGGL(e4m3_convert_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+    MAMBO_LAUNCH(e4m3_convert_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        in, n, out_sw, out_hw);
     return mambo_check_launch("e4m3_convert");
 }

@@ -119,7 +119,7 @@ extern "C" int mambo_synth_iq3s(uint64_t seed, int64_t blocks, int64_t row0, int
     MAMBO_REQUIRE(raw != nullptr && blocks >= 1 && nrows >= 1 && row0 >= 0, MAMBO_ERR_VALUE, "bad arguments");
     const int64_t total = nrows * blocks;
     MAMBO_REQUIRE((total + 255) / 256 <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "too many blocks for one launch");
-    hipLaunchKernelGGL(synth_iq3s_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+    MAMBO_LAUNCH(synth_iq3s_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        seed, blocks, row0, nrows, raw);
     return mambo_check_launch("synth_iq3s");
 }
@@ -129,7 +129,7 @@ extern "C" int mambo_synth_bf16(uint64_t seed, uint64_t outlier_seed, double out
 {
     MAMBO_REQUIRE(out != nullptr && count >= 1 && i0 >= 0, MAMBO_ERR_VALUE, "bad arguments");
     MAMBO_REQUIRE((count + 255) / 256 <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "count too large for one launch");
-    hipLaunchKernelGGL(synth_bf16_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+    MAMBO_LAUNCH(synth_bf16_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        seed, outlier_seed, outlier_frac, i0, count, out);
     return mambo_check_launch("synth_bf16");
 }

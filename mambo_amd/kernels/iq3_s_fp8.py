@@ -84,21 +84,16 @@ def iq3_s_table() -> np.ndarray:
 
 @lru_cache(maxsize=1)
 def iq3_s_fp8_table() -> np.ndarray:
-    """Pack positive magnitudes as E4M3 bits (iq3_s_fp8.py:77-94)."""
-    magnitudes = np.array([1, 3, 5, 7, 9, 11, 13, 15], dtype=np.uint8)
-    fp8_bits = np.array([0x38, 0x44, 0x4A, 0x4E, 0x51, 0x53, 0x55, 0x57], dtype=np.uint8)
-    lookup = np.zeros(256, dtype=np.uint8)
-    valid = np.zeros(256, dtype=np.bool_)
-    lookup[magnitudes] = fp8_bits
-    valid[magnitudes] = True
-    raw_table = iq3_s_table()
-    encoded_table = np.zeros_like(raw_table)
-    for shift in (0, 8, 16, 24):
-        magnitude = (raw_table >> shift) & 0xFF
-        if not np.all(valid[magnitude]):
-            raise ValueError("IQ3_S codebook contains a magnitude without an E4M3 encoding")
-        encoded_table |= lookup[magnitude].astype(np.uint32) << shift
-    return encoded_table
+    """The codebook with every magnitude byte replaced by its E4M3 bits
+    (iq3_s_fp8.py:77-94): the table the kernels decode with, as the library built it.
+    Raises ValueError if a codebook byte is not one of the odd magnitudes 1..15, which
+    are the ones with an exact E4M3 encoding."""
+    grid_bytes = iq3_s_table().view(np.uint8)
+    if np.any((grid_bytes & 1) == 0) or np.any(grid_bytes > 15):
+        raise ValueError("IQ3_S codebook contains a magnitude without an E4M3 encoding")
+    out = np.zeros(512, dtype=np.uint32)
+    _native.check(_native.lib().mambo_iq3s_fp8_grid(out.ctypes.data), "iq3_s_fp8_table")
+    return out
 
 
 def _get_iq3_table() -> torch.Tensor:
@@ -165,11 +160,18 @@ def _prepare_activations(x_values, x_scales, k: int):
         raise ValueError("x_scales must be uint8 [M,K/32]")
     if x_scales.device != x_values.device:
         raise ValueError("x_values and x_scales must be on the same device")
-    if x_values.stride(1) != 1 or x_values.stride(0) % 16 or x_values.data_ptr() % 16:
-        x_values = x_values.contiguous() if x_values.stride(1) != 1 else x_values.clone()
-    if x_scales.stride(1) != 1:
-        x_scales = x_scales.contiguous()
+    x_values = _aligned_rows(x_values, 16)
+    # the tiled kernel copies each token's 8 scale bytes of a block as two dwords
+    x_scales = _aligned_rows(x_scales, 8)
     return x_values, x_scales, m
+
+
+def _aligned_rows(t: torch.Tensor, align: int) -> torch.Tensor:
+    """`t` itself when its rows are unit-stride and start on `align`-byte boundaries,
+    else a contiguous copy (rows of K and K/32 bytes are multiples of 16 and 8)."""
+    if t.stride(1) == 1 and t.stride(0) % align == 0 and t.data_ptr() % align == 0:
+        return t
+    return torch.empty(t.shape, dtype=t.dtype, device=t.device).copy_(t)
 
 
 def _output(out, m: int, n: int, dev) -> torch.Tensor:

@@ -12,10 +12,12 @@ import torch
 
 from mambo_amd import _native
 
-# The gfx950 kernel has a fixed launch shape (four lanes per 32-element group, 64
-# groups per workgroup); tile_m / tile_k_groups are validated as in the reference
-# (powers of two) and otherwise do not change the result. The table keeps the
-# reference's "untuned architecture -> RuntimeError" rule (quantize_fp8.py:60-64).
+# Inert on gfx950: the kernel's launch shape is fixed (four lanes per 32-element group,
+# 64 groups per workgroup, two rows per workgroup iteration) and no entry of this table
+# changes it. The table is kept because the reference's launcher reads it: an
+# architecture without an entry raises RuntimeError (quantize_fp8.py:60-64), and
+# tile_m / tile_k_groups, given or looked up, are checked to be powers of two
+# (quantize_fp8.py:73-74) and then ignored.
 BEST_CONFIGS = {
     "gfx950": {
         "medium": {"tile_m": 4, "tile_k_groups": 4},

@@ -141,3 +141,29 @@ def inspect_gguf(path: str | os.PathLike[str]) -> dict[str, Any]:
     return {"gguf": {"version": version, "alignment": alignment, "data_offset": data_offset,
                      "tensor_count": n_tensors, "metadata_count": n_meta},
             "tensors": tensors}
+
+
+def read_block_matrix(path: str | os.PathLike[str], name: str, type_name: str):
+    """Bytes of the 2-D block-quantized tensor `name` as a host array u8
+    [rows, row_blocks, block_bytes] (ggml ne order [K, rows]: each row is K values in
+    K / block_elements blocks). ValueError if the file has no such tensor, if it is not
+    a 2-D `type_name` tensor, or if its sizes disagree with its block layout."""
+    import numpy as np
+
+    directory = {t["name"]: t for t in inspect_gguf(path)["tensors"]}
+    if name not in directory:
+        raise ValueError(f"GGUF has no tensor named {name!r}")
+    entry = directory[name]
+    kind = entry["type"]
+    if kind["name"] != type_name or len(entry["shape"]) != 2:
+        raise ValueError(f"{name} must be a 2D {type_name} tensor")
+    width, rows = entry["shape"]
+    per_block, block_bytes = kind["block_elements"], kind["block_bytes"]
+    row_blocks = width // per_block if per_block else 0
+    layout_ok = (per_block > 0 and block_bytes > 0 and row_blocks * per_block == width
+                 and entry["row_bytes"] == row_blocks * block_bytes
+                 and entry["n_bytes"] == rows * entry["row_bytes"])
+    if not layout_ok:
+        raise ValueError(f"{name} has an inconsistent GGUF block layout")
+    data = np.fromfile(path, dtype=np.uint8, count=entry["n_bytes"], offset=entry["offset"]["absolute"])
+    return data.reshape(rows, row_blocks, block_bytes)

@@ -10,7 +10,7 @@ so that each lane of a wave loads its decode inputs with a few contiguous loads.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -28,6 +28,12 @@ class IQ3SFields:
     signs: int32 [B,N,8]; scales: uint32 [B,N]. Total: 110 bytes/block.
     packed: uint8 tile layout consumed by the projection kernels (None until built;
     launch_iq3_s_fp8_matmul builds it from the fields on first use).
+
+    The packed tile is a cache of the SoA fields. It remembers which field tensors
+    (storage and in-place version) it was built from, and the launchers rebuild it when
+    a field has been written in place or replaced (``dataclasses.replace``) since. A
+    weight prepared with ``fields=False`` has placeholder fields; its packed tile is the
+    weight itself.
     """
 
     d: torch.Tensor
@@ -36,6 +42,19 @@ class IQ3SFields:
     signs: torch.Tensor
     scales: torch.Tensor
     packed: torch.Tensor | None = None
+    # fields_signature() of the SoA fields the packed tile was built from, or
+    # PACKED_ONLY (the fields are placeholders)
+    packed_from: tuple | None = field(default=None, repr=False, compare=False)
+
+
+PACKED_ONLY = ("packed-only",)
+
+
+def fields_signature(fields: IQ3SFields) -> tuple:
+    """Identity of the SoA field tensors: storage address, view offset and in-place
+    version counter of each (a write through any view of a tensor bumps its counter)."""
+    return tuple((t.untyped_storage().data_ptr(), t.storage_offset(), t._version)
+                 for t in _weight_kernel_args(fields))
 
 
 def _check_raw(iq3_weight) -> tuple[int, int]:
@@ -89,7 +108,9 @@ def prepare_iq3_s_fields(iq3_weight: torch.Tensor, *, fields: bool = True, strea
         _native.check(L.mambo_iq3s_prepare(iq3_weight.data_ptr(), n, blocks, sn, sb, sbyte, *ptrs,
                                            packed.data_ptr(), _native.stream_handle(stream)),
                       "prepare_iq3_s_fields")
-    return IQ3SFields(d, qs, qh, signs, scales, packed)
+    result = IQ3SFields(d, qs, qh, signs, scales, packed)
+    object.__setattr__(result, "packed_from", fields_signature(result) if fields else PACKED_ONLY)
+    return result
 
 
 def _weight_dimensions(iq3_weight: IQ3SFields) -> tuple[int, int]:
@@ -111,9 +132,19 @@ def _large_weight_kernel_args(iq3_weight: IQ3SFields) -> tuple[torch.Tensor, ...
             iq3_weight.signs.reshape(iq3_weight.signs.shape[0], -1), iq3_weight.scales)
 
 
+def packed_is_current(iq3_weight: IQ3SFields) -> bool:
+    """Whether the cached tile layout still holds the weight: it was built by
+    prepare_iq3_s_fields(fields=False) (then it is the weight), or from SoA field
+    tensors that are the current ones and have not been written in place since."""
+    if iq3_weight.packed is None or iq3_weight.packed_from is None:
+        return False
+    return iq3_weight.packed_from == PACKED_ONLY or iq3_weight.packed_from == fields_signature(iq3_weight)
+
+
 def ensure_packed(iq3_weight: IQ3SFields, stream=None) -> torch.Tensor:
-    """Tile layout of the weight, built from the SoA fields if it is not there yet."""
-    if iq3_weight.packed is not None:
+    """Tile layout of the weight: the cached one while packed_is_current, else rebuilt
+    from the current SoA fields (and cached)."""
+    if packed_is_current(iq3_weight):
         return iq3_weight.packed
     n, blocks = _weight_dimensions(iq3_weight)
     for name, t in zip(("d", "qs", "qh", "signs", "scales"), _weight_kernel_args(iq3_weight)):
@@ -126,4 +157,5 @@ def ensure_packed(iq3_weight: IQ3SFields, stream=None) -> torch.Tensor:
         _native.check(L.mambo_iq3s_pack(*(t.data_ptr() for t in _weight_kernel_args(iq3_weight)), n, blocks,
                                         packed.data_ptr(), _native.stream_handle(stream)), "pack")
     object.__setattr__(iq3_weight, "packed", packed)
+    object.__setattr__(iq3_weight, "packed_from", fields_signature(iq3_weight))
     return packed

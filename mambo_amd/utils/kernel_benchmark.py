@@ -31,10 +31,9 @@ from pathlib import Path
 from time import perf_counter
 from typing import Any, Callable, Sequence
 
-import numpy as np
 import torch
 
-from mambo_amd.utils.gguf import inspect_gguf
+from mambo_amd.utils.gguf import read_block_matrix
 
 Config = dict[str, Any]
 
@@ -102,6 +101,24 @@ def _time_events(stream, fn, iters: int) -> float:
     return start.elapsed_time(stop) * 1000.0 / iters
 
 
+def _host_time(stream, fn, *, drain_each: bool, warmup: int = 5, iters: int = 20) -> float:
+    """Host wall-clock microseconds per call of `fn` over `iters` calls after `warmup`
+    untimed ones. drain_each: the stream is synchronized after every call (the
+    reference's mean_us, launch + completion latency); otherwise once after the batch
+    (batched_us, throughput with queued launches)."""
+    def batch(calls: int) -> None:
+        for _ in range(calls):
+            fn()
+            if drain_each:
+                stream.synchronize()
+        stream.synchronize()
+
+    batch(warmup)
+    t0 = perf_counter()
+    batch(iters)
+    return (perf_counter() - t0) * 1e6 / iters
+
+
 def _time_config(case: BenchmarkCase, config: Config, *, warmup: int, iters: int, graph: bool) -> float:
     def once() -> None:
         if case.before_launch_fn is not None:
@@ -162,24 +179,8 @@ def mini_benchmark(cases: Sequence[BenchmarkCase], *, quiet: bool = False, graph
                 case.before_launch_fn(best)
             case.launch(best)
 
-        def measure(*, batched: bool) -> float:
-            for _ in range(5):
-                launch_once()
-                if not batched:
-                    case.stream.synchronize()
-            if batched:
-                case.stream.synchronize()
-            start = perf_counter()
-            for _ in range(20):
-                launch_once()
-                if not batched:
-                    case.stream.synchronize()
-            if batched:
-                case.stream.synchronize()
-            return (perf_counter() - start) * 1e6 / 20
-
-        mean_us = measure(batched=False)
-        batched_us = measure(batched=True)
+        mean_us = _host_time(case.stream, launch_once, drain_each=True)
+        batched_us = _host_time(case.stream, launch_once, drain_each=False)
         event_us = _time_events(case.stream, launch_once, 20)
         result = TuneResult(case.name, case.key, dict(best), mean_us, batched_us, event_us, tuner_us,
                             successes, failures, default_us,
@@ -218,25 +219,10 @@ def write_tuned_table(results: Sequence[TuneResult], path: Path, arch: str) -> N
 
 
 def load_gguf_weight(model: Path, weight_name: str, expected_type: str) -> torch.Tensor:
-    """Load a named 2D packed GGUF tensor as [N, K/block_elements, block_bytes] on the GPU
-    (kernel_benchmark.py:103-122)."""
-    manifest = inspect_gguf(model)
-    tensor = next((item for item in manifest["tensors"] if item["name"] == weight_name), None)
-    if tensor is None:
-        raise ValueError(f"GGUF has no tensor named {weight_name!r}")
-    quant_type = tensor["type"]
-    if quant_type["name"] != expected_type or len(tensor["shape"]) != 2:
-        raise ValueError(f"{weight_name} must be a 2D {expected_type} tensor")
-    k, n_rows = tensor["shape"]
-    block_values = quant_type["block_elements"]
-    block_bytes = quant_type["block_bytes"]
-    if (not block_values or not block_bytes or k % block_values
-            or tensor["row_bytes"] != k // block_values * block_bytes
-            or tensor["n_bytes"] != n_rows * tensor["row_bytes"]):
-        raise ValueError(f"{weight_name} has an inconsistent GGUF block layout")
-    raw = np.memmap(model, mode="r", dtype=np.uint8, offset=tensor["offset"]["absolute"],
-                    shape=(n_rows, k // block_values, block_bytes))
-    return torch.from_numpy(np.array(raw)).cuda()  # a writable host copy of the mapped bytes
+    """The named 2-D block-quantized GGUF tensor as u8 [N, K/block_elements, block_bytes]
+    on the current GPU (the reference's load_gguf_weight, kernel_benchmark.py:103-122;
+    same ValueErrors). The bytes are read on the host by gguf.read_block_matrix."""
+    return torch.from_numpy(read_block_matrix(model, weight_name, expected_type)).to("cuda")
 
 
 def synthetic_weight(n: int, k: int, seed: int = 0) -> torch.Tensor:

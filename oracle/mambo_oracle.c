@@ -239,8 +239,21 @@ int orc_mxfp8_exponent(float amax)
     return e;
 }
 
+/* Non-finite input is outside the reference's tests (fp8_reference.py:73-77 raises on
+ * it, ggml_reference.cpp:458-460 rejects it). The build's rule: a group holding a NaN
+ * or an infinity gets the E8M0 NaN scale 0xFF and, for every element, the E4M3 NaN
+ * 0x7F with the element's sign. */
 static void quantize_group(const float *v, uint8_t *q, uint8_t *s)
 {
+    int finite = 1;
+    for (int i = 0; i < 32; ++i)
+        finite &= isfinite(v[i]) != 0;
+    if (!finite) {
+        *s = 0xFF;
+        for (int i = 0; i < 32; ++i)
+            q[i] = (uint8_t)(0x7F | (signbit(v[i]) ? 0x80 : 0x00));
+        return;
+    }
     float amax = 0.0f;
     for (int i = 0; i < 32; ++i) {
         float a = fabsf(v[i]);
@@ -275,13 +288,15 @@ void orc_quantize_mxfp8_bf16(const uint16_t *x, int64_t m, int64_t k, int64_t ld
         }
 }
 
-/* MXFP8 -> f32: e4m3(q) * 2^(s-127); exact in f32 except below 2^-149. */
+/* MXFP8 -> f32: e4m3(q) * 2^(s-127); exact in f32 except below 2^-149. Scale byte
+ * 0xFF is the E8M0 NaN. */
 void orc_mxfp8_decode(const uint8_t *values, const uint8_t *scales, int64_t m, int64_t k, float *out)
 {
     for (int64_t r = 0; r < m; ++r)
-        for (int64_t c = 0; c < k; ++c)
-            out[r * k + c] = (float)ldexp((double)orc_e4m3_decode(values[r * k + c]),
-                                          (int)scales[r * (k / 32) + c / 32] - 127);
+        for (int64_t c = 0; c < k; ++c) {
+            const int s = scales[r * (k / 32) + c / 32];
+            out[r * k + c] = s == 0xFF ? NAN : (float)ldexp((double)orc_e4m3_decode(values[r * k + c]), s - 127);
+        }
 }
 
 /* ------------------------------------------------------------------- IQ3_S */

@@ -86,3 +86,45 @@ def test_gguf_weight_through_the_projection(gpu, tmp_path):
         load_gguf_weight(path, "missing", "iq3_s")
     with pytest.raises(ValueError, match="2D iq3_s"):
         load_gguf_weight(path, "output_norm.weight", "iq3_s")
+
+
+@pytest.mark.timeout(480)
+def test_benchmark_command_on_a_gguf_file(gpu, tmp_path, capsys):
+    """The reference's command line, verbatim (kernel_benchmark.py:131-141:
+    `iq3_s_fp8 --model M --weight-name NAME`), through the reference's module path, on a
+    GGUF file written here; then `python -m mambo.utils.kernel_benchmark ... --write-table`
+    in a process of its own, whose table holds a valid entry for each tuned shape."""
+    import ctypes
+    import json
+    import subprocess
+    import sys
+
+    from conftest import REPO
+    from mambo.kernels import iq3_s_fp8
+    from mambo_amd import _native
+    from mambo.utils.kernel_benchmark import benchmark_main
+    n, k = 96, 2048
+    path = tmp_path / "model.gguf"
+    write_gguf(path, [("blk.3.ffn_down.weight", [k, n], 21, oracle.gen_iq3s(33, n, k // 256).tobytes())])
+    step("benchmark_main iq3_s_fp8 --model ... --weight-name blk.3.ffn_down.weight")
+    results = benchmark_main(["iq3_s_fp8", "--model", str(path), "--weight-name", "blk.3.ffn_down.weight"])
+    text = capsys.readouterr().out
+    assert [r.case for r in results] == [f"M=4 N={n} K={k}", f"M=128 N={n} K={k}"]
+    for r in results:
+        assert f"{r.case}: best_config=" in text
+        assert r.mean_us > 0 and r.batched_us > 0 and r.event_us > 0 and not r.failures
+    assert "(warmup=5, iterations=20), candidates=" in text
+    table = tmp_path / "tuned.json"
+    step("python -m mambo.utils.kernel_benchmark ... --write-table")
+    run = subprocess.run([sys.executable, "-m", "mambo.utils.kernel_benchmark", "iq3_s_fp8", "--model", str(path),
+                          "--weight-name", "blk.3.ffn_down.weight", "--tokens", "4", "32",
+                          "--write-table", "--table", str(table)],
+                         cwd=REPO, capture_output=True, text=True, timeout=300)
+    assert run.returncode == 0, run.stderr[-2000:]
+    assert f"M=4 N={n} K={k}: best_config=" in run.stdout
+    written = json.loads(table.read_text())
+    assert set(written) == {"gfx950"}
+    for key, cfg in written["gfx950"].items():  # shapes whose default won have no entry
+        assert key in (iq3_s_fp8.tuned_key(n, k, 4), iq3_s_fp8.tuned_key(n, k, 32)), key
+        c = _native.GemmConfig.from_dict(cfg)
+        assert _native.lib().mambo_gemm_check_config(int(key.split("@")[1]), n, k // 256, ctypes.byref(c)) == 0

@@ -124,3 +124,27 @@ def test_fused_abi_leaves_mxfp8_buffers_alone_when_fused(gpu):
     with pytest.raises(ValueError, match="float32 or bfloat16"):
         from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_matmul_quantize
         launch_iq3_s_matmul_quantize(torch.zeros((1, k), dtype=torch.float16, device=gpu), fields)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fused_nonfinite_rows(gpu, dtype):
+    """Rows holding NaN or +-inf, quantized inside the projection and by the quantizer
+    launch: a row with a non-finite group (scale byte 0xFF, NaN codes) gives NaN in
+    every output of that row on both paths; the finite rows are bit-identical."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_matmul_quantize
+    raw, fields = weight(gpu, 256, 2048, seed=77)
+    gen = torch.Generator(device=gpu).manual_seed(77)
+    x = torch.randn((4, 2048), generator=gen, device=gpu)
+    x[1, 100] = float("inf")
+    x[3, 2047] = float("nan")
+    x[3, 5] = float("-inf")
+    x = x.to(dtype)
+    for cfg in CONFIGS:
+        step(f"fused non-finite rows {dtype} cfg={cfg}")
+        fused = launch_iq3_s_matmul_quantize(x, fields, config=cfg)
+        ref, (xv, xs) = two_step(x, fields, cfg)
+        torch.cuda.synchronize()
+        assert torch.isnan(fused[[1, 3]]).all() and torch.isnan(ref[[1, 3]]).all(), cfg
+        assert torch.equal(fused[[0, 2]], ref[[0, 2]]), cfg
+        assert torch.isfinite(fused[[0, 2]]).all(), cfg
+    assert int((xs.cpu() == 0xFF).sum()) == 3

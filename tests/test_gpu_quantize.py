@@ -114,3 +114,61 @@ def test_software_e4m3_path_matches_oracle(gpu):
                                                    _native.stream_handle(None)))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(sw.cpu().numpy(), oracle.e4m3_encode(x.astype(np.float64)))
+
+
+def test_hardware_e4m3_path(gpu):
+    """The quantizer's rounding (kQuantHwCvt: the hardware v_cvt_pk_fp8_f32) on every
+    value it can be fed, |y| <= 448: (1) all 2 x 1.14e9 float32 bit patterns in that
+    range through the hardware and the integer software path, compared on the GPU;
+    (2) every bf16 pattern in the range, every E4M3 midpoint (the ties) and the floats
+    next to them, hardware path against the oracle."""
+    from conftest import e4m3_values
+    from mambo_amd import _native
+    lib = _native.lib()
+    top = 0x43E00000  # 448.0f
+    chunk = 1 << 27
+    sw = torch.empty(chunk, dtype=torch.uint8, device=gpu)
+    hw = torch.empty(chunk, dtype=torch.uint8, device=gpu)
+    for sign in (0, -(1 << 31)):
+        step(f"e4m3 hardware vs software, every f32 pattern |x| <= 448, sign bit {int(sign != 0)}")
+        for lo in range(0, top + 1, chunk):
+            hi = min(lo + chunk, top + 1)
+            bits = torch.arange(lo, hi, dtype=torch.int32, device=gpu) | sign
+            n = hi - lo
+            _native.check(lib.mambo_e4m3_convert(bits.data_ptr(), n, sw.data_ptr(), hw.data_ptr(),
+                                                 _native.stream_handle(None)))
+            if not torch.equal(sw[:n], hw[:n]):
+                bad = torch.nonzero(sw[:n] != hw[:n])[:5, 0]
+                raise AssertionError(f"hardware and software E4M3 differ at f32 bits "
+                                     f"{[hex((int(b) + lo) | (sign & 0xFFFFFFFF)) for b in bad]}")
+        torch.cuda.synchronize()
+    bf16 = np.arange(0, 0x43E1, dtype=np.uint32) << 16
+    vals = e4m3_values()[:127]
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    x = np.concatenate([bf16.view(np.float32), mids, np.nextafter(mids, np.float32(0)),
+                        np.nextafter(mids, np.float32(1e9)), vals.astype(np.float32)])
+    x = np.concatenate([x, -x]).astype(np.float32)
+    xt = torch.from_numpy(x).to(gpu)
+    out = torch.empty(x.size, dtype=torch.uint8, device=gpu)
+    step(f"e4m3 hardware path against the oracle on {x.size} values")
+    _native.check(lib.mambo_e4m3_convert(xt.data_ptr(), x.size, None, out.data_ptr(), _native.stream_handle(None)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.e4m3_encode(x.astype(np.float64)))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_nonfinite_groups(gpu, dtype):
+    """Groups holding NaN or +-inf: scale byte 0xFF and E4M3 NaN codes with the input's
+    signs; the other groups of the same rows quantize as usual (oracle rule)."""
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    from test_oracle import nonfinite_rows
+    x = torch.from_numpy(nonfinite_rows()).to(gpu).to(dtype)
+    step(f"quantize non-finite rows {dtype}")
+    q, s = launch_quantize_fp8(x)
+    torch.cuda.synchronize()
+    host = x.cpu()
+    eq, es = oracle.quantize_mxfp8(host.numpy() if dtype == torch.float32 else host.view(torch.int16).numpy()
+                                   .view(np.uint16))
+    np.testing.assert_array_equal(s.cpu().numpy(), es)
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    assert (es == 0xFF).sum() == 5

@@ -169,6 +169,39 @@ def test_quantizer_ties_round_to_even():
     assert vals[v[0, 1]] == 8.0 and vals[v[0, 2]] == 10.0 and vals[v[0, 3]] == -10.0
 
 
+def nonfinite_rows() -> np.ndarray:
+    """Rows with non-finite groups (the build's rule; outside the reference's tests):
+    group 0 holds +inf among finite values, group 1 a NaN, group 2 -inf and a NaN,
+    group 3 is finite (and must quantize as usual), group 4 only infinities."""
+    x = np.random.default_rng(3).standard_normal((2, 160)).astype(np.float32)
+    x[0, 5] = np.inf
+    x[0, 32 + 9] = np.nan
+    x[0, 64 + 1] = -np.inf
+    x[0, 64 + 30] = np.nan
+    x[0, 128:160] = np.where(np.arange(32) % 2, np.inf, -np.inf)
+    x[1, 31] = -np.inf
+    return x
+
+
+def test_quantizer_nonfinite_groups_known_answers():
+    """A group holding NaN or +-inf: scale byte 0xFF (E8M0 NaN) and, for each element,
+    the E4M3 NaN 0x7F with the element's sign; every other group is unaffected."""
+    x = nonfinite_rows()
+    v, s = oracle.quantize_mxfp8(x)
+    sign = np.where(np.signbit(x), 0x80, 0).astype(np.uint8)
+    for r, g in ((0, 0), (0, 1), (0, 2), (0, 4), (1, 0)):
+        assert s[r, g] == 0xFF, (r, g)
+        np.testing.assert_array_equal(v[r, 32 * g:32 * g + 32], 0x7F | sign[r, 32 * g:32 * g + 32])
+    finite = np.ones_like(s, dtype=bool)
+    finite[0, [0, 1, 2, 4]] = False
+    finite[1, 0] = False
+    clean = np.where(np.isfinite(x), x, 0).astype(np.float32)
+    cv, cs = oracle.quantize_mxfp8(clean)
+    np.testing.assert_array_equal(s[finite], cs[finite])
+    np.testing.assert_array_equal(v.reshape(2, 5, 32)[finite], cv.reshape(2, 5, 32)[finite])
+    assert np.all(np.isnan(oracle.mxfp8_decode(v, s).reshape(2, 5, 32)[~finite]))
+
+
 def test_bf16_input_equals_f32_input():
     bits = oracle.gen_bf16(5, 16 * 256, outlier_frac=0.01).reshape(16, 256)
     f = oracle.bf16_to_f32(bits)
