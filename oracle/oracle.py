@@ -8,6 +8,9 @@ cpu_baseline leg of bench.py use it as the checker. The product package
 from __future__ import annotations
 
 import ctypes
+import io
+import json
+import math
 import os
 import subprocess
 from pathlib import Path
@@ -189,3 +192,51 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
 
 def default_threads() -> int:
     return len(os.sched_getaffinity(0))
+
+
+# ------------------------------------------------------------------ command-line tool
+CLI_PATH = HERE / "mambo_oracle_cli"
+CLI_ARRAYS = ("dequant_rows", "ggml_dequant_f64", "mxfp8_f64")
+
+
+def read_cli_packet(packet: bytes, *, m: int, k: int, n: int, rows: int) -> tuple[dict, dict]:
+    """Parse mambo_oracle_cli's stdout: a u8 .npy array of JSON metadata, then the three
+    float32 arrays it lists, nothing after them (the checks of the reference harness,
+    compute_reference_gguf.py:124-151)."""
+    stream = io.BytesIO(packet)
+    meta = np.load(stream, allow_pickle=False)
+    if meta.dtype != np.uint8 or meta.ndim != 1 or not 0 < meta.size <= 1 << 16:
+        raise ValueError("oracle CLI stdout has invalid NumPy metadata")
+    header = json.loads(meta.tobytes().decode("utf-8"))
+    if header.get("schema_version") != 1 or header.get("op") != "matmul":
+        raise ValueError("oracle CLI stdout uses an unsupported schema or op")
+    shapes = {"dequant_rows": [rows, k], "ggml_dequant_f64": [m, n], "mxfp8_f64": [m, n]}
+    if [d.get("name") for d in header.get("arrays", [])] != list(CLI_ARRAYS):
+        raise ValueError("oracle CLI stdout has an unexpected array table")
+    arrays = {}
+    for d in header["arrays"]:
+        name, shape = d["name"], shapes[d["name"]]
+        a = np.load(stream, allow_pickle=False)
+        if d.get("dtype") != "float32" or d.get("shape") != shape or d.get("nbytes") != 4 * math.prod(shape):
+            raise ValueError(f"oracle CLI stdout has invalid metadata for {name}")
+        if a.dtype != np.dtype("<f4") or list(a.shape) != shape or not a.flags.c_contiguous:
+            raise ValueError(f"oracle CLI stdout has an invalid NumPy array for {name}")
+        arrays[name] = a
+    if stream.read(1):
+        raise ValueError("oracle CLI stdout has trailing bytes")
+    return arrays, header
+
+
+def cli_matmul(model, weight: str, x: np.ndarray, *, dequant_rows: int = 4) -> tuple[dict, dict]:
+    """Run mambo_oracle_cli on float32 activations x [M, K] and parse its arrays."""
+    x = np.ascontiguousarray(x, dtype="<f4")
+    if not CLI_PATH.exists():
+        build()
+    run = subprocess.run([str(CLI_PATH), "--op", "matmul", "--model", str(model), "--weight", weight,
+                          "--m", str(x.shape[0]), "--dequant-rows", str(dequant_rows)],
+                         input=x.tobytes(), capture_output=True, check=False)
+    if run.returncode != 0:
+        raise RuntimeError(f"oracle CLI failed: {run.stderr.decode(errors='replace').strip()}")
+    meta = np.load(io.BytesIO(run.stdout), allow_pickle=False)
+    k, n = json.loads(meta.tobytes().decode())["shape_ggml_ne_order"]
+    return read_cli_packet(run.stdout, m=x.shape[0], k=k, n=n, rows=dequant_rows)
