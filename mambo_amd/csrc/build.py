@@ -3,7 +3,9 @@
     python -m mambo_amd.csrc.build          # or mambo_amd.csrc.build.build()
 
 Each translation unit is compiled in parallel with hipcc into ``_build/`` and linked
-into ``mambo_amd/libmambo_hip.so`` (in-tree, so it travels with the repository).
+into ``mambo_amd/libmambo_hip.so`` (in-tree, so it travels with the repository). The
+C++ manifest loader ``mambo_amd/mambo_loadtest`` and the runtime ABI manifests
+(``mambo_amd/abi/*.abi.json``, mambo_amd/abi.py) are built next to it.
 """
 
 from __future__ import annotations
@@ -19,6 +21,7 @@ CSRC = Path(__file__).resolve().parent
 PKG = CSRC.parent
 REPO = PKG.parent
 OUT = PKG / "libmambo_hip.so"
+LOADTEST = PKG / "mambo_loadtest"
 BUILD_DIR = CSRC / "_build"
 ARCH = "gfx950"
 
@@ -65,7 +68,23 @@ def build(extra_flags: list[str] | None = None, jobs: int | None = None) -> Path
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, OUT)
+    build_loadtest()
+    from mambo_amd import abi
+    abi.write_manifests()
     return OUT
+
+
+def build_loadtest() -> Path:
+    """The C++ manifest loader (csrc/loadtest.cpp): host code only, linked against the
+    HIP runtime, zlib and libdl; it dlopens the library rather than linking it."""
+    tmp = LOADTEST.with_suffix(".tmp")
+    cmd = [hipcc(), "-O2", "-std=c++20", f"-I{REPO / 'include'}", str(CSRC / "loadtest.cpp"), "-o", str(tmp),
+           "-lz", "-ldl"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for loadtest.cpp:\n{proc.stderr}")
+    os.replace(tmp, LOADTEST)
+    return LOADTEST
 
 
 if __name__ == "__main__":
