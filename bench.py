@@ -77,48 +77,53 @@ def synth_activation(m: int, k: int, seed: int):
     return (*launch_quantize_fp8(rows), rows)
 
 
-def build_gemm_workload(args):
-    """Weights, activations and outputs of the projection sweep, as a list of launches.
-    Each launch is (names, [(n, k, fields, out)], (x_values, x_scales)); projections of
-    one layer that read the same input (q/k/v, gate/up) share a launch unless
-    args.no_group."""
+def build_weights(workload: str, layers: int):
+    """The sweep's distinct IQ3_S weights (packed form only), generated on the GPU:
+    [(layer, name, n, k, slot, fields)], seed 1000*layer + index in the layer."""
     import torch
-    shapes = LLAMA70B_LAYER if args.workload == "llama70b" else LLAMA8B_LAYER
-    layers = args.layers
-    m = args.m
-    acts = {}
-    for _, n, k, slot in shapes:
-        if slot not in acts:
-            acts[slot] = synth_activation(m, k, seed=1 + slot)
-    outs = {}
-    launches = []
+    shapes = LLAMA70B_LAYER if workload == "llama70b" else LLAMA8B_LAYER
+    weights = []
     t0 = time.time()
     for layer in range(layers):
         for j, (name, n, k, slot) in enumerate(shapes):
-            fields = synth_weight(n, k, seed=1000 * layer + j)
-            key = (name, n, k)
-            if key not in outs:
-                outs[key] = torch.empty((m, n), dtype=torch.float32, device="cuda")
-            proj = (n, k, fields, outs[key])
-            if (not args.no_group and launches and launches[-1][3] == (layer, slot)
-                    and len(launches[-1][1]) < 4):
-                launches[-1][0].append(name)
-                launches[-1][1].append(proj)
-            else:
-                launches.append(([name], [proj], acts[slot], (layer, slot)))
+            weights.append((layer, name, n, k, slot, synth_weight(n, k, seed=1000 * layer + j)))
         if layer % 10 == 9:
             log(f"prepared {layer + 1}/{layers} layers ({time.time() - t0:.1f} s)")
+    torch.cuda.synchronize()
+    return weights
+
+
+def build_launches(weights, m: int, no_group: bool):
+    """Activations, outputs and the launch list of one step at m tokens. Each launch is
+    (names, [(n, k, fields, out)], (x_values, x_scales, bf16 rows)); projections of one
+    layer that read the same input (q/k/v, gate/up) share a launch unless no_group."""
+    import torch
+    acts, outs, launches = {}, {}, []
+    for layer, name, n, k, slot, fields in weights:
+        if slot not in acts:
+            acts[slot] = synth_activation(m, k, seed=1 + slot)
+        key = (name, n, k)
+        if key not in outs:
+            outs[key] = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        proj = (n, k, fields, outs[key])
+        if not no_group and launches and launches[-1][3] == (layer, slot) and len(launches[-1][1]) < 4:
+            launches[-1][0].append(name)
+            launches[-1][1].append(proj)
+        else:
+            launches.append(([name], [proj], acts[slot], (layer, slot)))
     torch.cuda.synchronize()
     return [(names, projs, act) for names, projs, act, _ in launches]
 
 
-def run_gemm(args):
+def run_gemm(args, weights=None):
     import torch
     from mambo_amd.kernels.iq3_s_fp8 import (launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped,
                                              launch_iq3_s_matmul_quantize, select_config)
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
 
-    launches = build_gemm_workload(args)
+    if weights is None:
+        weights = build_weights(args.workload, args.layers)
+    launches = build_launches(weights, args.m, args.no_group)
     projections = [p for (_, projs, _) in launches for p in projs]
     configs = [select_config(args.m, sum(n for n, _, _, _ in projs), projs[0][1]) for (_, projs, _) in launches]
     weight_bytes = sum(f.packed.numel() for (_, _, f, _) in projections)
@@ -194,30 +199,50 @@ def run_gemm(args):
     }
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds: float, unit: str = "GB/s") -> dict:
     """Oracle restatement of the reference CPU path on its CPU case: one IQ3_S linear
     N=K=4096 (seed-0 counter-based blocks), M=8 bf16 ~N(0,1) activations quantized to
-    MXFP8, IQ3_S to_float + float64-accumulated dot per output (all host cores).
-    Reported in the unit of the GPU line (GB/s of algorithmic bytes, or TFLOP/s)."""
-    import numpy as np
+    MXFP8, IQ3_S to_float + float64-accumulated dot per output. Timed on all host cores
+    this process may use (OpenMP), then on one thread. Reported in the unit of the GPU
+    line (GB/s of algorithmic bytes, or TFLOP/s)."""
     from oracle import oracle
     n = k = 4096
     m = 8
     raw = oracle.gen_iq3s(0, n, k // 256)
     xv, xs = oracle.quantize_mxfp8(oracle.gen_bf16(1, m * k).reshape(m, k))
+
+    def timed(threads: int, budget: float):
+        iters, t0 = 0, time.perf_counter()
+        while True:
+            oracle.iq3s_fp8_matmul(xv, xs, raw, threads=threads)
+            iters += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+        return iters, (time.perf_counter() - t0) / iters
+
+    def rate(per: float) -> float:
+        return 2 * m * n * k / per / 1e12 if unit == "TFLOP/s" else proj_bytes(m, n, k) / per / 1e9
+
     threads = len(os.sched_getaffinity(0))
-    iters, t0 = 0, time.perf_counter()
-    while True:
-        oracle.iq3s_fp8_matmul(xv, xs, raw, threads=threads)
-        iters += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    per = (time.perf_counter() - t0) / iters
-    value = 2 * m * n * k / per / 1e12 if unit == "TFLOP/s" else proj_bytes(m, n, k) / per / 1e9
-    return {"value": round(value, 6), "unit": unit, "cores": threads, "kind": "port",
+    iters, per = timed(threads, seconds)
+    iters1, per1 = timed(1, seconds / 2)
+    return {"value": round(rate(per), 6), "unit": unit, "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "single_thread": {"value": round(rate(per1), 6), "unit": unit, "cores": 1,
+                              "ms_per_run": round(per1 * 1e3, 2), "runs": iters1},
             "sample": f"one IQ3_S linear N=K=4096, M=8 (the reference CPU case): {iters} runs in {per * iters:.1f} s "
-                      f"({per * 1e3:.1f} ms each) of the oracle's to_float + f64-dot restatement "
-                      f"of ggml_reference.cpp:495-523 on {threads} threads"}
+                      f"({per * 1e3:.1f} ms each) on {threads} threads, {iters1} runs ({per1 * 1e3:.1f} ms each) on "
+                      f"1 thread, of the oracle's to_float + f64-dot restatement of ggml_reference.cpp:495-523"}
 
 
 def run_quant(args):
@@ -434,6 +459,75 @@ def measured_traffic(workload: str):
     return None
 
 
+def gemm_workload_name(args) -> str:
+    grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
+    if args.with_quant != "none":
+        grouping += {"separate": ", a quantizer launch before each GEMM launch",
+                     "fused": ", quantization inside the GEMM launch where it fits (M <= 4)"}[args.with_quant]
+    model = "llama3-70b" if args.workload == "llama70b" else "llama3-8b"
+    return f"{model} projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
+
+
+def roofline_of(r: dict, mfma_bound: bool, workload: str) -> dict:
+    """roofline object of one measurement: achieved = algorithmic work per launch / the
+    average launch time over the timed region (HIP events on the launch stream)."""
+    if mfma_bound:
+        value = r["tflops"]
+        return {"bound": "mfma", "achieved": round(value, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(value / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic(workload),
+                "algorithmic_flops_per_launch": round(r["step_flops"] / r["launches"]),
+                "avg_launch_us": round(r["per_launch_us"], 3)}
+    value = r["value"]
+    return {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
+            "algorithmic_bytes_per_launch": round(r["per_launch_bytes"]),
+            "avg_launch_us": round(r["per_launch_us"], 3)}
+
+
+# Further points of the M = 1..8192 metric timed by the default run, after the headline:
+# the Llama-3-70B sweep at 16 tokens (same weights) and the Llama-3-8B sweep at the two
+# prefill sizes (32 layers, 3.0 GB of weights built after the 70B ones are freed).
+DEFAULT_POINTS = "llama70b:16,llama8b:2048,llama8b:8192"
+
+
+def sweep_points(args, held: list) -> list:
+    """Time the --points list (workload:m, ...) with the same steps, warmup and
+    grouping as the headline. held = [the headline's weights]: reused for points of
+    the same workload, emptied (and the memory returned) before other weights are
+    built."""
+    import argparse as _ap
+    import torch
+    spec = args.points
+    if spec == "auto":
+        headline = args.workload == "llama70b" and args.m == 1 and args.layers == 80 and args.with_quant == "none"
+        spec = DEFAULT_POINTS if headline else "none"
+    if spec == "none":
+        return []
+    out = []
+    held_key = (args.workload, args.layers)
+    for item in spec.split(","):
+        wl, m = item.split(":")
+        sub = _ap.Namespace(**vars(args))
+        sub.workload, sub.m = wl, int(m)
+        sub.layers = 80 if wl == "llama70b" else 32
+        key = (sub.workload, sub.layers)
+        if key != held_key:
+            held.clear()
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            held.append(build_weights(sub.workload, sub.layers))
+            held_key = key
+        log(f"point {wl} M={m}")
+        r = run_gemm(sub, held[0])
+        mfma_bound = sub.m >= PREFILL_M
+        name = gemm_workload_name(sub)
+        out.append({"workload": name, "m": sub.m, "value": round(r["tflops"] if mfma_bound else r["value"], 2),
+                    "unit": "TFLOP/s" if mfma_bound else "GB/s", "ms_per_step": round(r["ms"], 4),
+                    "gbs": round(r["value"], 2), "tflops": round(r["tflops"], 3),
+                    "roofline": roofline_of(r, mfma_bound, name)})
+    return out
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -450,6 +544,9 @@ def main(argv=None) -> int:
                         "quantized once before timing, as the reference times the matmul alone")
     p.add_argument("--no-group", action="store_true",
                    help="one launch per projection (default: q/k/v and gate/up share a launch)")
+    p.add_argument("--points", default="auto",
+                   help="further workload:m points timed after the headline, comma-separated, or 'none' "
+                        f"(auto: {DEFAULT_POINTS} when the headline is the default 70B M=1 sweep)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args(argv)
@@ -460,6 +557,7 @@ def main(argv=None) -> int:
               file=sys.stderr)
         return 2
     rank = int(os.environ.get("RANK", "0"))
+    points = []
 
     import torch
     from mambo_amd import _native
@@ -502,34 +600,23 @@ def main(argv=None) -> int:
         config = {"workload": workload, "m": 4096, "k": 4096}
         dtype, data = "bf16 -> fp8-e4m3 + e8m0", "synthetic (bf16 ~N(0,1), 0.1% x100 outliers)"
     else:
-        r = run_gemm(args)
+        weights = build_weights(args.workload, args.layers)
+        r = run_gemm(args, weights)
         metric = ("fused IQ3_S x MXFP8 GEMM TFLOP/s vs MX-FP8 MFMA roofline" if args.m >= PREFILL_M else
                   "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline")
-        grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
         if args.with_quant != "none":
             metric += " (bf16 activations quantized in the step)"
-            grouping += {"separate": ", a quantizer launch before each GEMM launch",
-                         "fused": ", quantization inside the GEMM launch where it fits (M <= 4)"}[args.with_quant]
-        if args.workload == "llama70b":
-            workload = f"llama3-70b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
-        else:
-            workload = f"llama3-8b projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
+        workload = gemm_workload_name(args)
         config = {"workload": workload, "m": args.m, "projections_per_step": r["projections"],
                   "launches_per_step": r["launches"], "weight_gb": round(r["weight_bytes"] / 1e9, 3),
                   "tflops": round(r["tflops"], 3), "graph": not args.no_graph}
+        held = [weights]  # sweep_points drops the headline weights before building others
+        del weights
+        points = sweep_points(args, held)
     mfma_bound = (args.workload in ("llama70b", "llama8b") and args.m >= PREFILL_M) or args.workload == "mfma"
     value = r["tflops"] if mfma_bound else r["value"]
     unit = "TFLOP/s" if mfma_bound else "GB/s"
-    if mfma_bound:
-        roofline = {"bound": "mfma", "achieved": round(value, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(value / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic(workload),
-                    "algorithmic_flops_per_launch": round(r["step_flops"] / r["launches"]),
-                    "avg_launch_us": round(r["per_launch_us"], 3)}
-    else:
-        roofline = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
-                    "algorithmic_bytes_per_launch": round(r["per_launch_bytes"]),
-                    "avg_launch_us": round(r["per_launch_us"], 3)}
+    roofline = roofline_of(r, mfma_bound, workload)
     line = {
         "metric": metric,
         "value": round(value, 2),
@@ -546,6 +633,8 @@ def main(argv=None) -> int:
         "config": config,
         "roofline": roofline,
     }
+    if points:
+        line["points"] = points
     if rank == 0 and not args.no_cpu_baseline:
         log("timing the CPU baseline")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds, unit)

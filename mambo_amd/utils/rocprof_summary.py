@@ -5,6 +5,17 @@ Two reports, both plain text meant to be committed next to the numbers they back
 * ``stats``: the per-kernel duration table of a ``rocprofv3 --kernel-trace --stats
   --output-format csv`` run (``*_kernel_stats.csv``), plus a combined row for every
   kernel whose name contains ``--family`` (template instantiations of one kernel).
+* ``window``: from the per-dispatch ``*_kernel_trace.csv`` of the same kind of run,
+  the last ``--last`` dispatches whose kernel name contains ``--family`` (the timed
+  replays of a benchmark, which come after its eager, check and warm-up launches): their
+  average duration, their span from first start to last end, and the rate that the
+  algorithmic work per launch gives over each.
+* ``mfma``: MFMA counters per dispatch of a ``--pmc`` run (``SQ_VALU_MFMA_BUSY_CYCLES``,
+  ``SQ_INSTS_VALU_MFMA_MOPS_F8``, ``GRBM_GUI_ACTIVE``) and optionally of a second run of
+  rocprofiler's derived ``MfmaUtil``: MFMA busy fraction over all SIMDs and executed F8
+  MFMA flops against the algorithmic ones. The CSV's ``GRBM_GUI_ACTIVE`` is the sum over
+  the XCDs (MfmaUtil's formula takes the maximum), so the busy fraction divides by the
+  per-XCD mean.
 * ``traffic``: HBM bytes per dispatch from two ``--pmc`` runs (``FETCH_SIZE``, then
   ``WRITE_SIZE``) of a workload, each scaled by what the same counter reads for the plain
   copy kernel (``mambo_copy_bytes``) over a known number of bytes in two more runs. The
@@ -120,6 +131,94 @@ def traffic_report(args) -> None:
     print("\n".join(lines))
 
 
+def kernel_trace(directory: str) -> list[dict]:
+    """Dispatch rows of the kernel_trace CSV in start order: name, start_ns, end_ns."""
+    rows = []
+    with open(_one(directory, "_kernel_trace.csv"), newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append({"name": r["Kernel_Name"], "start": int(r["Start_Timestamp"]), "end": int(r["End_Timestamp"])})
+    rows.sort(key=lambda r: r["start"])
+    return rows
+
+
+def window_report(args) -> None:
+    rows = [r for r in kernel_trace(args.dir) if args.family in r["name"]]
+    if len(rows) < args.last:
+        raise ValueError(f"only {len(rows)} {args.family} dispatches, asked for the last {args.last}")
+    win = rows[-args.last:]
+    durs = [r["end"] - r["start"] for r in win]
+    avg_ns = sum(durs) / len(durs)
+    span_ns = win[-1]["end"] - win[0]["start"]
+    per_launch_ns = span_ns / args.last
+    unit, scale = ("TFLOP/s", 1e-3) if args.unit == "flops" else ("GB/s", 1.0)
+    work = args.work_per_launch
+    by_name: dict[str, list[int]] = {}
+    for r, d in zip(win, durs):
+        by_name.setdefault(r["name"], []).append(d)
+    lines = [f"# rocprofv3 kernel trace, timed window: {args.title}", "", "Command:", "", "```", args.command, "```",
+             "", f"All dispatches of `{args.family}` in the trace: {len(rows)}; the window is the last {args.last} "
+             f"({args.note}).", "",
+             "| kernel | dispatches in window | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for name, d in sorted(by_name.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{_short(name)}` | {len(d)} | {sum(d) / len(d) / 1e3:.3f} | {min(d) / 1e3:.3f} | "
+                     f"{max(d) / 1e3:.3f} |")
+    try:
+        stats = kernel_stats(args.dir)
+    except FileNotFoundError:
+        stats = []
+    if stats:
+        lines += ["", "Whole run (`--stats`, every dispatch including set-up, eager and warm-up launches):", "",
+                  "| kernel | calls | total ms | avg us |", "|---|---|---|---|"]
+        for r in stats[:8]:
+            lines.append(f"| `{_short(r['name'])}` | {r['calls']} | {r['total_ns'] / 1e6:.3f} | {r['avg_ns'] / 1e3:.3f} |")
+    lines += ["", f"Window: average kernel duration {avg_ns / 1e3:.3f} us; span {span_ns / 1e6:.3f} ms = "
+                  f"{per_launch_ns / 1e3:.3f} us per launch (kernel plus the gap to the next one).", "",
+              f"Algorithmic work per launch {work:,.0f} {'flop' if args.unit == 'flops' else 'B'}: "
+              f"{work / avg_ns * scale:.1f} {unit} over the average kernel duration, "
+              f"{work / per_launch_ns * scale:.1f} {unit} over the span."]
+    Path(args.out).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+SIMD_PER_CU = 4
+
+
+def mfma_report(args) -> None:
+    busy = counter_per_dispatch(args.dir, "SQ_VALU_MFMA_BUSY_CYCLES", args.family)
+    mops = counter_per_dispatch(args.dir, "SQ_INSTS_VALU_MFMA_MOPS_F8", args.family)
+    gui = counter_per_dispatch(args.dir, "GRBM_GUI_ACTIVE", args.family)
+    if not len(busy) == len(mops) == len(gui):
+        raise ValueError("counter records do not pair up per dispatch")
+    simds = args.cus * SIMD_PER_CU
+    util = [b / (g / args.xcds * simds) for b, g in zip(busy, gui)]
+    derived = counter_per_dispatch(args.util_dir, "MfmaUtil", args.family) if args.util_dir else []
+    executed = [m_ * 512 for m_ in mops]
+    mean = lambda v: sum(v) / len(v)  # noqa: E731
+    rec = {"workload": args.workload, "kernel_family": args.family, "dispatches": len(busy), "cus": args.cus,
+           "mfma_busy": mean(util), "mfma_busy_min": min(util), "mfma_busy_max": max(util),
+           "mfma_util_rocprof": mean(derived) / 100 if derived else None,
+           "executed_f8_flops_per_dispatch": mean(executed),
+           "algorithmic_flops_per_dispatch": args.algorithmic_flops,
+           "executed_over_algorithmic": mean(executed) / args.algorithmic_flops if args.algorithmic_flops else None,
+           "command": args.command}
+    out = Path(args.out)
+    out.with_suffix(".json").write_text(json.dumps(rec, indent=1) + "\n")
+    lines = [f"# MFMA counters per dispatch: {args.workload}", "", "Command:", "", "```", args.command, "```", "",
+             f"Kernel family `{args.family}`, {len(busy)} dispatches.", "",
+             "| counter (per dispatch, mean) | value |", "|---|---|",
+             f"| SQ_VALU_MFMA_BUSY_CYCLES (sum over SIMDs) | {mean(busy):,.0f} |",
+             f"| GRBM_GUI_ACTIVE | {mean(gui):,.0f} |",
+             f"| SQ_INSTS_VALU_MFMA_MOPS_F8 (x512 = F8 flops) | {mean(mops):,.0f} |", "",
+             f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {args.xcds} XCDs x {simds} SIMDs): mean "
+             f"{100 * rec['mfma_busy']:.1f}% (min {100 * min(util):.1f}%, max {100 * max(util):.1f}%)."
+             + (f" rocprofv3's derived MfmaUtil in a run of its own: mean {mean(derived):.1f}%." if derived else ""),
+             "",
+             f"Executed F8 MFMA flops {mean(executed):,.0f} per dispatch against {args.algorithmic_flops:,} "
+             f"algorithmic (ratio {rec['executed_over_algorithmic']:.3f})."]
+    out.with_suffix(".md").write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -137,8 +236,27 @@ def main(argv=None) -> int:
     t.add_argument("--algorithmic-bytes", type=int, required=True)
     t.add_argument("--family", default="gemm_stream_kernel")
     t.add_argument("--calib-family", default="copy_bytes_kernel")
+    w = sub.add_parser("window")
+    w.add_argument("dir")
+    w.add_argument("--family", required=True)
+    w.add_argument("--last", type=int, required=True)
+    w.add_argument("--work-per-launch", type=float, required=True)
+    w.add_argument("--unit", choices=["bytes", "flops"], default="bytes")
+    w.add_argument("--title", default="")
+    w.add_argument("--note", default="the timed replays")
+    w.add_argument("--command", required=True)
+    w.add_argument("--out", required=True)
+    m = sub.add_parser("mfma")
+    m.add_argument("dir")
+    m.add_argument("--family", required=True)
+    m.add_argument("--cus", type=int, default=256)
+    m.add_argument("--xcds", type=int, default=8)
+    m.add_argument("--util-dir", default="")
+    m.add_argument("--algorithmic-flops", type=int, required=True)
+    for name in ("--workload", "--command", "--out"):
+        m.add_argument(name, required=True)
     args = p.parse_args(argv)
-    (stats_report if args.cmd == "stats" else traffic_report)(args)
+    {"stats": stats_report, "traffic": traffic_report, "window": window_report, "mfma": mfma_report}[args.cmd](args)
     return 0
 
 
