@@ -47,6 +47,7 @@ __constant__ SplitTables c_split = kSplitTables;
 #define MAMBO_STREAM_DEPTH 2
 #endif
 constexpr int kDepth = MAMBO_STREAM_DEPTH;
+
 #ifndef MAMBO_SCHED_FENCE
 #define MAMBO_SCHED_FENCE 1
 #endif
@@ -1206,75 +1207,188 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     }
 }
 
-// ---------------------------------------------------------------------------- register-staged form
-// The 256-token tile (MT=16): its two 68 KiB buffers leave no room for a third, so the
-// block copied into LDS must be one requested a block earlier; this form loads block b+2
-// into registers during block b and stores it at the top of block b+1 instead (two
-// blocks of latency cover), into double-buffered dynamic LDS with a 272-byte row pitch
-// (the 16 rows read by one lane group start in different banks). Measured 3-9% faster
-// than the direct copy for this tile, and slower than it for the smaller ones.
-constexpr int kTiledPitch = 272;
+// ---------------------------------------------------------------------------- prefill form
+// 256 tokens x 16*W weight rows (W waves of 16 rows, one workgroup per CU), with the
+// decode of block b+1 spread over the MFMAs of block b inside each wave:
+//  * step mt (mt = 0..15) of block b: the four MFMAs of 16-token sub-tile mt (K halves x
+//    hi/lo, one accumulator chain), then the activation fragments and scales of sub-tile
+//    mt+1 are requested, the codebook word of code mt of block b+1 is requested and code
+//    mt-1 is finished (two perms, two sign ops), and sub-tile mt-1's result is scaled by
+//    d into its accumulators. Every wait is for something requested a step earlier (about
+//    128 MFMA cycles), and each step issues ~12 VALU instructions against four MFMAs.
+//  * the decoded operands of two blocks (current and next, 2 x 32 VGPRs) and the packed
+//    weights of the next two blocks are held: block b issues the copies of block b+1's
+//    activations, then the loads of block b+2's weights, so every wait is partial (the
+//    decode waits for loads issued a block earlier, the barrier for the copies only);
+//    the block loop is unrolled by two so the operand sets swap without moves.
+//  * each lane reads both activation scale bytes of a sub-tile with one 16-bit load and
+//    the MFMA picks byte h with op_sel; the codebook, the split table and the scale
+//    buffers lie below 64 KiB of LDS so their addresses fold into the offset field.
+// 2 waves per SIMD at W = 8 (256 VGPRs per wave).
+// LDS of the prefill form: one __shared__ array per buffer, so the compiler can tell the
+// copy target (buffer C^1) from the buffer being read (C) and does not wait for the copies
+// before reading; the tables and scale buffers are declared first and land below 64 KiB.
+struct PrefillLds {
+    static constexpr int kRows = 256;
+};
 
-__host__ __device__ constexpr int tiled_lds_bytes(int MT)
+// Decoded operands of one 16-row weight tile for one block, in the dense K order.
+struct Decoded {
+    v8i hi[2], lo[2];
+    float d;
+};
+
+// Per-code pieces of the decode (decode_split split into steps).
+struct DecodeState {
+    uint32_t s[5];   // index bit stream
+    uint32_t p[2];   // transposed sign words of the lane's two groups
+    uint4 tab[2];    // split-table entries of the two groups' scale nibbles
+    uint16_t dh;
+};
+
+__device__ __forceinline__ void decode_begin(DecodeState &st, const WTile &w, const uint4 *split)
 {
-    return 2 * (16 * MT * kTiledPitch + 16 * MT * 8);
+    st.s[0] = w.ia.x;
+    st.s[1] = w.ia.y;
+    st.s[2] = w.ia.z;
+    st.s[3] = w.ia.w;
+    st.s[4] = (uint32_t)w.ib;
+    st.p[0] = w.sg.x;
+    st.p[1] = w.sg.y;
+    st.tab[0] = split[w.sc & 15u];
+    st.tab[1] = split[(uint32_t)w.sc >> 4];
+    st.dh = w.dh;
 }
 
-// MT x NT sub-tiles of one block: A fragments from the staged block (a: values at this
-// lane's row/column offset, sa: scales), one chain of four MFMAs (K halves x hi/lo) per
-// sub-tile, then the block's d in f32. The fence per sub-tile keeps the compiler from
-// hoisting every LDS read of the block into registers.
-template <int MT, int NT>
-__device__ __forceinline__ void mfma_block_pitched(const uint8_t *a, const uint8_t *sa, const v8i (&bh)[NT][2],
-                                           const v8i (&bl)[NT][2], const float (&d)[NT], float (&acc)[MT][NT][4])
+template <int I>
+__device__ __forceinline__ uint32_t decode_fetch(const DecodeState &st, const uint8_t *lvl)
 {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const uint8_t *ar = a + 16 * mt * kTiledPitch;
-        const uint8_t *sr = sa + 16 * mt * 8;
-        v8i av[2];
-        int sc[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint4 lo = *reinterpret_cast<const uint4 *>(ar + 32 * h);
-            const uint4 hi = *reinterpret_cast<const uint4 *>(ar + 32 * h + 64);
-            av[h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-            sc[h] = sr[h];
-        }
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-            v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bh[nt][0], zero, 0, 0, 0, sc[0], 0, 128);
-            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[0], bl[nt][0], c, 0, 0, 0, sc[0], 0, 128);
-            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bh[nt][1], c, 0, 0, 0, sc[1], 0, 128);
-            c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[1], bl[nt][1], c, 0, 0, 0, sc[1], 0, 128);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                acc[mt][nt][r] = __builtin_fmaf(c[r], d[nt], acc[mt][nt][r]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    return *reinterpret_cast<const uint32_t *>(lvl + code_addr<I>(st.s));
+}
+
+template <int I>
+__device__ __forceinline__ void decode_finish(const DecodeState &st, uint32_t lv, Decoded &out)
+{
+    constexpr int H = I / 8, C = I % 8;
+    int hi, lo;
+    split_word<C>(lv, st.p[H], st.tab[H], hi, lo);
+    out.hi[H][C] = hi;
+    out.lo[H][C] = lo;
+    if constexpr (C == 7) {
+        to_dense_order(out.hi[H]);
+        to_dense_order(out.lo[H]);
     }
 }
 
-template <int MT, int NT, int W>
-__global__ __launch_bounds__(W * 64) void gemm_tiled_regs_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
-                                                            const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
-                                                            GroupArgs ga, int B, int bps, int atomic)
+// Copies of block b's activations into one buffer of the prefill LDS (values `vals`, scales
+// `scl`): value copy j of a wave moves 4 rows (1 KiB, offsets voff[j]), waves 0..7 one
+// scale copy each.
+template <int W>
+__device__ __forceinline__ void prefill_stage(uint8_t *vals, uint8_t *scl, int b, __amdgpu_buffer_rsrc_t xrows,
+                                              __amdgpu_buffer_rsrc_t srows, const uint32_t (&voff)[256 / 4 / W],
+                                              uint32_t soff_stage, int wave)
 {
-    constexpr int kRows = 16 * MT;
-    constexpr int kABytes = kRows * kTiledPitch;
-    constexpr int kSBytes = kRows * 8;
+#pragma unroll
+    for (int j = 0; j < 256 / 4 / W; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrows, (lds_ptr)(vals + 1024 * (wave + W * j)), 16, voff[j], 256u * b,
+                                                 0, 0);
+    if (wave < PrefillLds::kRows / 32)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(srows, (lds_ptr)(scl + 256 * wave), 4, soff_stage, 8u * b, 0, 0);
+}
+
+// Sub-tiles whose activation fragments are requested ahead of their MFMAs.
+#ifndef MAMBO_PREFILL_AHEAD
+#define MAMBO_PREFILL_AHEAD 2
+#endif
+constexpr int kPrefillAhead = MAMBO_PREFILL_AHEAD;
+
+// Operands of one prefill block in flight: activation fragments and scales of
+// kPrefillAhead + 1 sub-tiles (slots), codebook words of two codes, the previous
+// sub-tile's result.
+struct PrefillPipe {
+    v8i a[kPrefillAhead + 1][2];
+    int sc[kPrefillAhead + 1];
+    uint32_t lw[2];
+    v4f prev;
+};
+
+__device__ __forceinline__ void prefill_load(PrefillPipe &pp, int slot, const uint8_t *ar, const uint32_t (&ao)[2][2],
+                                             const uint8_t *sr)
+{
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 lo = *reinterpret_cast<const uint4 *>(ar + ao[h][0]);
+        const uint4 hi = *reinterpret_cast<const uint4 *>(ar + ao[h][1]);
+        pp.a[slot][h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+    pp.sc[slot] = (int)*reinterpret_cast<const uint16_t *>(sr);
+}
+
+// Step mt of a prefill block (see gemm_prefill_kernel): sub-tile mt's MFMAs with operands
+// `cur`, the next sub-tile's loads, code mt of the next block's decode requested and code
+// mt-1 finished into `nxt`, sub-tile mt-1 scaled into its accumulators.
+template <int mt>
+__device__ __forceinline__ void prefill_step(PrefillPipe &pp, const Decoded &cur, Decoded &nxt, const DecodeState &st,
+                                             const uint8_t *vals, const uint8_t *scl, const uint32_t (&ao)[2][2],
+                                             uint32_t soff, const uint8_t *lvl, float d, float (&acc)[16][4])
+{
+    constexpr int sl = mt % (kPrefillAhead + 1), cw = mt & 1;
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(pp.a[sl][0], cur.hi[0], zero, 0, 0, 0, pp.sc[sl], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(pp.a[sl][0], cur.lo[0], c, 0, 0, 0, pp.sc[sl], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(pp.a[sl][1], cur.hi[1], c, 0, 0, 1, pp.sc[sl], 0, 128);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(pp.a[sl][1], cur.lo[1], c, 0, 0, 1, pp.sc[sl], 0, 128);
+    if constexpr (mt + kPrefillAhead < 16)
+        prefill_load(pp, (mt + kPrefillAhead) % (kPrefillAhead + 1), vals + 4096 * (mt + kPrefillAhead), ao,
+                     scl + 128 * (mt + kPrefillAhead) + soff);
+    pp.lw[cw] = decode_fetch<mt>(st, lvl);
+    if constexpr (mt > 0) {
+        decode_finish<mt - 1>(st, pp.lw[cw ^ 1], nxt);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[mt - 1][r] = __builtin_fmaf(pp.prev[r], d, acc[mt - 1][r]);
+    }
+    pp.prev = c;
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int... MT>
+__device__ __forceinline__ void prefill_steps(PrefillPipe &pp, const Decoded &cur, Decoded &nxt, const DecodeState &st,
+                                              const uint8_t *vals, const uint8_t *scl, const uint32_t (&ao)[2][2],
+                                              uint32_t soff, const uint8_t *lvl, float d, float (&acc)[16][4],
+                                              std::integer_sequence<int, MT...>)
+{
+    (prefill_step<MT>(pp, cur, nxt, st, vals, scl, ao, soff, lvl, d, acc), ...);
+}
+
+template <int... I>
+__device__ __forceinline__ void decode_all(const DecodeState &st, const uint8_t *lvl, Decoded &out,
+                                           std::integer_sequence<int, I...>)
+{
+    ((decode_finish<I>(st, decode_fetch<I>(st, lvl), out)), ...);
+}
+
+template <int W>
+__global__ __launch_bounds__(W * 64) void gemm_prefill_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
+                                                              GroupArgs ga, int B, int bps, int atomic)
+{
+    using L = PrefillLds;
+    constexpr int kRows = L::kRows;
     constexpr int kThreads = W * 64;
-    constexpr int kChunks = kRows * 16;                     // 16-byte chunks of one A block
-    constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
-    extern __shared__ __align__(16) uint8_t smem[];          // A[2][kABytes], S[2][kSBytes]
+    constexpr int kVCopies = kRows / 4 / W;   // 1 KiB value copies per wave and block
+    constexpr int kSCopies = kRows / 32;      // 256-byte scale copies per block (waves 0..kSCopies-1)
+    static_assert(kRows / 4 % W == 0 && kSCopies <= W, "staging must spread evenly over the waves");
     __shared__ uint32_t s_lvl[512];
     __shared__ uint4 s_split[16];
+    __shared__ __align__(16) uint8_t s_scale0[kRows * 8];
+    __shared__ __align__(16) uint8_t s_scale1[kRows * 8];
+    __shared__ __align__(16) uint8_t s_vals0[kRows * 256];
+    __shared__ __align__(16) uint8_t s_vals1[kRows * 256];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, q = lane >> 4;
 
-    // this workgroup's projection; tile_begin counts workgroups here
     const uint8_t *packed = ga.packed[0];
     float *out = ga.out[0];
     int64_t N = ga.n[0], ldo = ga.ldo[0], wg = blockIdx.x;
@@ -1289,128 +1403,112 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_regs_kernel(const uint8_t *
         }
     const int64_t tiles = (N + kTileRows - 1) / kTileRows;
     const int64_t m0 = (int64_t)blockIdx.y * kRows;
-    // weight tiles of this wave (clamped to the last tile; stores are masked)
-    __amdgpu_buffer_rsrc_t wt[NT];
-    int64_t tile[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        tile[nt] = wg * (NT * W) + wave * NT + nt;
-        wt[nt] = byte_rsrc(packed + min(tile[nt], tiles - 1) * (int64_t)B * kTileBytes);
-    }
+    const int64_t tile = wg * W + wave;
+    const __amdgpu_buffer_rsrc_t wt = byte_rsrc(packed + min(tile, tiles - 1) * (int64_t)B * kTileBytes);
 
     for (int i = tid; i < 512; i += kThreads)
         s_lvl[i] = c_grid.level[i];
     if (tid < 16)
         s_split[tid] = uint4{c_split.w[tid][0], c_split.w[tid][1], c_split.w[tid][2], c_split.w[tid][3]};
 
-    // A staging: chunk c of block b = row c >> 4 (clamped to M-1), bytes 16*(c & 15);
-    // thread tid owns chunks tid + j*kThreads.
-    uint4 stage[kPerThread];
-    uint2 sstage = {0u, 0u};
-    const __amdgpu_buffer_rsrc_t xtile = byte_rsrc(xv + m0 * ldxv); // rows past M are clamped to row M-1
-    const int64_t last_row = M - 1 - m0;
-    // scales: thread tid stages row min(tid, kRows-1); the threads past kRows rewrite the
-    // last row's identical bytes, which keeps the staging branch-free
-    const int srow_ = min(tid, kRows - 1);
-    const uint8_t *ssrc = xs + min(m0 + srow_, M - 1) * ldxs;
-    // (fold expressions over an index sequence: every staging register has a
-    // compile-time index, so the array stays in registers across iterations)
-    constexpr auto kJ = std::make_integer_sequence<int, kPerThread>{};
-    auto load_one = [&](int j, int b) -> uint4 {
-        const int c = min(tid + j * kThreads, kChunks - 1);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-            xtile, (uint32_t)min<int64_t>(c >> 4, last_row) * (uint32_t)ldxv + 16u * (c & 15), 256u * b, 0);
-        return uint4{v[0], v[1], v[2], v[3]};
-    };
-    auto store_one = [&](int j, int buf, uint4 v) {
-        const int c = tid + j * kThreads;
-        if (kChunks % kThreads == 0 || c < kChunks)
-            *reinterpret_cast<uint4 *>(smem + buf * kABytes + (c >> 4) * kTiledPitch + 16 * (c & 15)) = v;
-    };
-#define MAMBO_LOAD_STAGE(b)                                                                                        \
-    do {                                                                                                           \
-        [&]<int... J>(std::integer_sequence<int, J...>) { ((stage[J] = load_one(J, (b))), ...); }(kJ);             \
-        sstage = *reinterpret_cast<const uint2 *>(ssrc + 8 * (int64_t)(b));                                        \
-    } while (0)
-#define MAMBO_STORE_STAGE(buf)                                                                                     \
-    do {                                                                                                           \
-        [&]<int... J>(std::integer_sequence<int, J...>) { (store_one(J, (buf), stage[J]), ...); }(kJ);             \
-        *reinterpret_cast<uint2 *>(smem + 2 * kABytes + (buf) * kSBytes + 8 * srow_) = sstage;                     \
-    } while (0)
-
-    // A operand offsets of this lane inside a staged block (token row col of each
-    // sub-tile; see the dense kernel for the byte and scale order)
-    const uint32_t xo = 32u * (4 * (q >> 1)) + 16u * (q & 1), so = 4u * (q & 1) + 2u * (q >> 1);
-
-    float acc[MT][NT][4];
+    // Staging: value copy j of this wave moves rows 4*(wave + W*j) .. +3 (16 bytes per
+    // lane, chunk slot lane&15 of row r holds source chunk (lane&15) ^ (r&15)); rows past M
+    // read row M-1. Offsets are loop-invariant; the block offset goes in the scalar offset.
+    const __amdgpu_buffer_rsrc_t xrows = byte_rsrc(xv + m0 * ldxv), srows = byte_rsrc(xs + m0 * ldxs);
+    const int last_row = (int)min<int64_t>(M - 1 - m0, kRows - 1);
+    uint32_t voff[kVCopies];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                acc[mt][nt][r] = 0.0f;
+    for (int j = 0; j < kVCopies; ++j) {
+        const int row = 4 * (wave + W * j) + (lane >> 4);
+        voff[j] = (uint32_t)min(row, last_row) * (uint32_t)ldxv + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    }
+    const uint32_t soff_stage = (uint32_t)min(32 * wave + (lane >> 1), last_row) * (uint32_t)ldxs + 4u * (lane & 1);
 
-    // Pipeline: in iteration b the staging registers hold block b+1 (loaded one iteration
-    // earlier) and are written to LDS at the top, then refilled with block b+2; the
-    // loads are consumed only in the next iteration, so they overlap a whole block of
-    // math and cannot be moved down to their stores.
+    // A operand of lane (token row col of a sub-tile, q), K half h: 16-byte chunks
+    // 8*(q>>1) + (q&1) + 2h and +4 of the row at their swizzled slots (the dense kernel's
+    // K order); its scale bytes for h = 0, 1 are adjacent at soff.
+    uint32_t ao[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp)
+            ao[h][pp] = 256u * col + 16u * ((8u * (q >> 1) + (q & 1) + 2u * h + 4u * pp) ^ (uint32_t)col);
+    const uint32_t soff = 8u * col + 4u * (q & 1) + 2u * (q >> 1);
+
+    float acc[16][4];
+#pragma unroll
+    for (int mt = 0; mt < 16; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[mt][r] = 0.0f;
+
     const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
-    const uint32_t aoff = (uint32_t)col * kTiledPitch + xo, soff = (uint32_t)col * 8 + so;
-    // K range of this workgroup: blocks [b0, b1) (grid z splits K; partial sums are
-    // added into an output zeroed beforehand)
     const int b0 = blockIdx.z * bps, b1 = min(B, b0 + bps);
-    WTile wcur[NT], wnext[NT];
-    v8i bh[NT][2], bl[NT][2];
-    float d[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-        wcur[nt] = load_w_rsrc<0>(wt[nt], (uint32_t)b0 * kTileBytes, lane, col);
-    MAMBO_LOAD_STAGE(b0);
-    MAMBO_STORE_STAGE(b0 & 1);
-    MAMBO_LOAD_STAGE(min(b0 + 1, b1 - 1));
+    auto wblock = [&](int b) { return (uint32_t)min(b, b1 - 1) * kTileBytes; };
+    // packed weights: block b0 decoded up front, b0+1 in slot 0; block b requests block
+    // b+2's weights into the slot its predecessor decoded from, right after its activation
+    // copies (vector memory completes in issue order: the decode waits only for loads a
+    // block old, the barrier only for the copies)
+    WTile wslot[2];
+    Decoded dec[2];
+    {
+        const WTile w0 = load_w_rsrc<0>(wt, wblock(b0), lane, col);
+        wslot[0] = load_w_rsrc<0>(wt, wblock(b0 + 1), lane, col);
+        prefill_stage<W>(s_vals0, s_scale0, b0, xrows, srows, voff, soff_stage, wave);
+        __syncthreads(); // codebook and split tables
+        DecodeState st;
+        decode_begin(st, w0, s_split);
+        decode_all(st, lvl, dec[0], std::make_integer_sequence<int, 16>{});
+        dec[0].d = half_bits_to_float(st.dh);
+    }
     __syncthreads();
 
+    // Block b with operands dec[C] (decoding block b+1 from wslot[C] into dec[C^1]);
+    // buffer C (= (b - b0) & 1) holds block b's activations. A macro, so C is a constant:
+    // the two operand sets are fixed registers and the two buffers fixed arrays.
+#define MAMBO_PREFILL_BLOCK(C)                                                                                     \
+    do {                                                                                                           \
+        const uint8_t *vals_ = (C) ? s_vals1 : s_vals0;                                                            \
+        const uint8_t *scl_ = (C) ? s_scale1 : s_scale0;                                                           \
+        prefill_stage<W>((C) ? s_vals0 : s_vals1, (C) ? s_scale0 : s_scale1, min(b + 1, b1 - 1), xrows, srows,     \
+                         voff, soff_stage, wave);                                                                  \
+        wslot[(C) ^ 1] = load_w_rsrc<0>(wt, wblock(b + 2), lane, col);                                             \
+        DecodeState st_;                                                                                           \
+        decode_begin(st_, wslot[C], s_split);                                                                      \
+        PrefillPipe pp_;                                                                                           \
+        for (int t_ = 0; t_ < kPrefillAhead; ++t_)                                                                 \
+            prefill_load(pp_, t_, vals_ + 4096 * t_, ao, scl_ + 128 * t_ + soff);                                  \
+        prefill_steps(pp_, dec[C], dec[(C) ^ 1], st_, vals_, scl_, ao, soff, lvl, dec[C].d, acc,                   \
+                      std::make_integer_sequence<int, 16>{});                                                      \
+        decode_finish<15>(st_, pp_.lw[1], dec[(C) ^ 1]);                                                           \
+        dec[(C) ^ 1].d = half_bits_to_float(st_.dh);                                                               \
+        for (int r = 0; r < 4; ++r)                                                                                \
+            acc[15][r] = __builtin_fmaf(pp_.prev[r], dec[C].d, acc[15][r]);                                        \
+        __syncthreads();                                                                                           \
+    } while (0)
     for (int b = b0; b < b1; ++b) {
-        // buffer (b+1)&1 was last read in block b-1, before the previous barrier; after
-        // the last block this fills the idle buffer
-        MAMBO_STORE_STAGE((b + 1) & 1);
-        MAMBO_LOAD_STAGE(min(b + 2, b1 - 1));
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-            wnext[nt] = load_w_rsrc<0>(wt[nt], (uint32_t)min(b + 1, b1 - 1) * kTileBytes, lane, col);
-        __builtin_amdgcn_sched_barrier(0);
-        decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);
-        mfma_block_pitched<MT, NT>(smem + (b & 1) * kABytes + aoff, smem + 2 * kABytes + (b & 1) * kSBytes + soff, bh, bl, d,
-                           acc);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-            wcur[nt] = wnext[nt];
-        __syncthreads();
+        MAMBO_PREFILL_BLOCK(0);
+        if (++b == b1)
+            break;
+        MAMBO_PREFILL_BLOCK(1);
     }
+#undef MAMBO_PREFILL_BLOCK
 
-    // D[i][j] of sub-tile (mt, nt): lane j + 16*(i/4), register i%4 -> token
-    // m0 + 16*mt + 4q + r, weight row 16*tile + col.
+    const int64_t n = tile * kTileRows + col;
+    if (n < N) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const int64_t n = tile[nt] * kTileRows + col;
-        if (n >= N)
-            continue;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < 16; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t m = m0 + 16 * mt + 4 * q + r;
                 if (m < M) {
                     if (atomic)
-                        atomicAdd(out + m * ldo + n, acc[mt][nt][r]);
+                        atomicAdd(out + m * ldo + n, acc[mt][r]);
                     else
-                        __builtin_nontemporal_store(acc[mt][nt][r], out + m * ldo + n); // written once
+                        __builtin_nontemporal_store(acc[mt][r], out + m * ldo + n); // written once
                 }
             }
     }
-#undef MAMBO_LOAD_STAGE
-#undef MAMBO_STORE_STAGE
 }
 
 // Zero row blockIdx.y of projection blockIdx.z's output (the split-K accumulators of
@@ -1551,10 +1649,10 @@ template <int MT, int NT, int W>
 void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
                     int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
-    if constexpr (MT >= 16 && W <= 8) // 256 x 128 x 8: register staging
-        MAMBO_LAUNCH((gemm_tiled_regs_kernel<MT, NT, W>), grid, dim3(W * 64), tiled_lds_bytes(MT), stream, xv,
-                           ldxv, xs, ldxs, M, ga, B, bps, atomic);
-    else // direct copies; 256 x 256 x 16 in the half-K form
+    if constexpr (MT >= 16 && NT == 1 && W == 8) // 256 x 128 x 8: the pipelined prefill form
+        MAMBO_LAUNCH((gemm_prefill_kernel<W>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs, ldxs, M, ga, B, bps,
+                     atomic);
+    else // direct copies; the 256-token tiles of 256 weight rows in the half-K form
         MAMBO_LAUNCH((gemm_tiled_kernel<MT, NT, W, (MT >= 16)>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs,
                            ldxs, M, ga, B, bps, atomic);
 }
@@ -1691,6 +1789,12 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
             c.tile_m = 256;
             c.tile_n = 256;
             c.waves = 16;
+        } else if (fits256 && (wgs = cdiv(rt, 8) * cdiv(m, 256)) >= kCUs * 7 / 8 &&
+                   wgs * 8 >= cdiv(wgs, kCUs) * kCUs * 7) {
+            // the 256 x 128 x 8 prefill form where the 256-row tile leaves CUs idle but
+            // the 128-row one fills whole rounds (8B o and down projections at 2048 tokens:
+            // 4-10% ahead of 128 x 128 x 8)
+            c.tile_m = 256;
         } else if (fits128 && ((wgs = cdiv(rt, 8) * cdiv(m, 128)) >= kCUs || long_k)) {
             c.tile_m = 128;
             if (long_k && wgs < 2 * kCUs)

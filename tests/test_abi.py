@@ -124,11 +124,13 @@ def test_gemm_config_defaults_and_validation():
         assert lib.mambo_gemm_check_config(32, 4096, 16, ctypes.byref(c)) == rc, fields
     # prefill default: 256 x 256 x 16 waves when every round of its grid (one workgroup
     # per CU) fills at least 7/8 of the CUs (and the tokens are padded by at most 1/8 more
-    # than with 128-token tiles), else
+    # than with 128-token tiles), else 256 x 128 x 8 under the same rule, else
     # 128 x 128 x 8 when that gives every CU a workgroup (padding at most 1/8 over 64-token
     # tiles), else 64 x 128 x 8; on long K (>= 48 blocks) the 128-token tile with K split
     # until the grid covers the chip twice
-    for m, n, blocks, tile, split in ((2048, 4096, 32, (128, 128, 8), 1), (8192, 14336, 32, (256, 256, 16), 1),
+    for m, n, blocks, tile, split in ((2048, 4096, 32, (256, 128, 8), 1), (2048, 4096, 16, (256, 128, 8), 1),
+                                      (2048, 4096, 56, (256, 128, 8), 1), (8192, 4096, 16, (256, 256, 16), 1),
+                                      (8192, 14336, 32, (256, 256, 16), 1),
                                       (512, 8192, 32, (128, 128, 8), 1), (512, 57344, 32, (256, 256, 16), 1),
                                       (512, 28672, 16, (256, 256, 16), 1), (2048, 6144, 16, (128, 128, 8), 1),
                                       (2048, 10240, 32, (128, 128, 8), 1), (8192, 10240, 32, (256, 256, 16), 1),
