@@ -362,6 +362,39 @@ def test_prefill_shape_sampled(gpu, n, k):
     assert np.all(np.isfinite(out))
 
 
+@pytest.mark.parametrize("m,k,split", [(700, 2048, 4), (700, 1024, 4), (1100, 1024, 1)])
+def test_prefill_form_many_items(gpu, m, k, split):
+    """The 256-token x 128-row prefill form with more work items than CUs, so each
+    workgroup runs several items through one pipeline: a ragged last token tile (rows
+    past M read as zero and are not stored), ragged last weight groups, K splits of two
+    blocks and of one block (the block after next then lies two items ahead), and a
+    grouped launch into column slices of one buffer. Sampled weight rows against the
+    oracle; the columns around the slices and the rows past M keep their contents."""
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul_grouped
+    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    n1, n2 = 3000, 4100
+    step(f"synth weights {n1}+{n2} x {k}")
+    fields = [_synth_weight(gpu, n1, k, seed=11), _synth_weight(gpu, n2, k, seed=12)]
+    xq, xs = launch_quantize_fp8(_synth_act(gpu, m, k, seed=13))
+    cfg = {"kernel": _native.GEMM_TILED, "waves": 8, "split_k": split, "tile_m": 256, "tile_n": 128}
+    big = torch.full((m + 5, n1 + n2 + 40), 7.0, dtype=torch.float32, device=gpu)
+    c1, c2 = 8, 24 + n1
+    step(f"grouped prefill form M={m} K={k} cfg={cfg}")
+    launch_iq3_s_fp8_matmul_grouped(xq, xs, fields, outs=[big[:m, c1:c1 + n1], big[:m, c2:c2 + n2]], config=cfg)
+    torch.cuda.synchronize()
+    b = big.cpu().numpy()
+    assert np.all(b[m:] == 7.0) and np.all(b[:, :c1] == 7.0)
+    assert np.all(b[:, c1 + n1:c2] == 7.0) and np.all(b[:, c2 + n2:] == 7.0)
+    xqn, xsn = xq.cpu().numpy(), xs.cpu().numpy()
+    for seed, n, c in ((11, n1, c1), (12, n2, c2)):
+        rng = np.random.default_rng(seed + m)
+        rows = np.unique(np.concatenate([rng.choice(n, 20, replace=False), [0, 127, 128, n - 1]]))
+        raw = np.concatenate([oracle.gen_iq3s(seed, 1, k // 256, row0=int(r)) for r in rows])
+        expected = oracle.iq3s_fp8_matmul(xqn, xsn, raw, threads=oracle.default_threads())
+        check(b[:m, c + rows], expected, elementwise=False)
+
+
 def test_default_32_token_tiles(gpu):
     """17-32 tokens on a wide enough grid: the library default is the tiled kernel's
     32-token tile (four waves sharing each activation block) with K split."""
