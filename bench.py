@@ -9,7 +9,9 @@ generator, streamed once per step at M tokens (default M=1, decode). One step = 
 share a grouped launch; --no-group launches each alone), replayed from a captured HIP
 graph; MXFP8 activations are quantized once before timing (the reference times the
 matmul alone, iq3_s_fp8.py:402-465). --workload llama8b runs the same sweep over the
-32 layers of Llama-3-8B (3.0 GB of weights).
+32 layers of Llama-3-8B (3.0 GB of weights). --tp G sweeps one GPU's shard of a
+G-way tensor-parallel layer (N/G rows of the column-parallel projections, K/G columns of
+the row-parallel ones).
 
 value = algorithmic bytes per step / step time, with
   bytes per projection = N*K*110/256 (IQ3_S weights) + M*K*33/32 (E4M3 + E8M0 activations)
@@ -22,7 +24,7 @@ linear N=K=4096 with M=8, timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--m M]
                     [--workload llama70b|llama8b|quant|copy|read|readsweep|mfma]
-                    [--layers L] [--no-group] [--no-graph] [--with-quant none|separate|fused]
+                    [--layers L] [--tp G] [--no-group] [--no-graph] [--with-quant none|separate|fused]
 """
 
 from __future__ import annotations
@@ -77,11 +79,32 @@ def synth_activation(m: int, k: int, seed: int):
     return (*launch_quantize_fp8(rows), rows)
 
 
-def build_weights(workload: str, layers: int):
+def layer_shapes(workload: str, tp: int = 1) -> list:
+    """(name, N, K, input slot) of one layer's linears; with tp > 1, one GPU's shard of a
+    tensor-parallel layer: the column-parallel projections (q/k/v, gate/up: slots 0 and 2)
+    keep N/tp rows, the row-parallel ones (o, down: slots 1 and 3) K/tp columns, whole
+    256-weight blocks (their partial outputs would be summed across GPUs)."""
+    shapes = LLAMA70B_LAYER if workload in ("llama70b", "readsweep") else LLAMA8B_LAYER
+    if tp == 1:
+        return shapes
+    out = []
+    for name, n, k, slot in shapes:
+        if slot in (0, 2):
+            if n % (16 * tp):
+                raise ValueError(f"{name}: N={n} does not split into {tp} shards of whole 16-row tiles")
+            out.append((name, n // tp, k, slot))
+        else:
+            if k % (256 * tp):
+                raise ValueError(f"{name}: K={k} does not split into {tp} shards of whole 256-weight blocks")
+            out.append((name, n, k // tp, slot))
+    return out
+
+
+def build_weights(workload: str, layers: int, tp: int = 1):
     """The sweep's distinct IQ3_S weights (packed form only), generated on the GPU:
     [(layer, name, n, k, slot, fields)], seed 1000*layer + index in the layer."""
     import torch
-    shapes = LLAMA70B_LAYER if workload == "llama70b" else LLAMA8B_LAYER
+    shapes = layer_shapes(workload, tp)
     weights = []
     t0 = time.time()
     for layer in range(layers):
@@ -122,7 +145,7 @@ def run_gemm(args, weights=None):
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
 
     if weights is None:
-        weights = build_weights(args.workload, args.layers)
+        weights = build_weights(args.workload, args.layers, args.tp)
     launches = build_launches(weights, args.m, args.no_group)
     projections = [p for (_, projs, _) in launches for p in projs]
     configs = [select_config(args.m, sum(n for n, _, _, _ in projs), projs[0][1]) for (_, projs, _) in launches]
@@ -357,7 +380,7 @@ def run_read(args):
 def sweep_launch_bytes(args) -> list:
     """Packed IQ3_S bytes each launch of the projection sweep reads (the grouping of
     build_gemm_workload: q/k/v and gate/up share a launch unless args.no_group)."""
-    shapes = LLAMA70B_LAYER if args.workload in ("llama70b", "readsweep") else LLAMA8B_LAYER
+    shapes = layer_shapes(args.workload, args.tp)
     sizes = []
     for _ in range(args.layers):
         prev = None
@@ -467,7 +490,8 @@ def gemm_workload_name(args) -> str:
         grouping += {"separate": ", a quantizer launch before each GEMM launch",
                      "fused": ", quantization inside the GEMM launch where it fits (M <= 4)"}[args.with_quant]
     model = "llama3-70b" if args.workload == "llama70b" else "llama3-8b"
-    return f"{model} projection sweep: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
+    shard = f" (one GPU's shard at tensor parallelism {args.tp})" if args.tp > 1 else ""
+    return f"{model} projection sweep{shard}: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
 
 
 def roofline_of(r: dict, mfma_bound: bool, workload: str) -> dict:
@@ -501,23 +525,24 @@ def sweep_points(args, held: list) -> list:
     import torch
     spec = args.points
     if spec == "auto":
-        headline = args.workload == "llama70b" and args.m == 1 and args.layers == 80 and args.with_quant == "none"
+        headline = (args.workload == "llama70b" and args.m == 1 and args.layers == 80 and args.with_quant == "none"
+                    and args.tp == 1)
         spec = DEFAULT_POINTS if headline else "none"
     if spec == "none":
         return []
     out = []
-    held_key = (args.workload, args.layers)
+    held_key = (args.workload, args.layers, args.tp)
     for item in spec.split(","):
         wl, m = item.split(":")
         sub = _ap.Namespace(**vars(args))
         sub.workload, sub.m = wl, int(m)
         sub.layers = 80 if wl == "llama70b" else 32
-        key = (sub.workload, sub.layers)
+        key = (sub.workload, sub.layers, sub.tp)
         if key != held_key:
             held.clear()
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
-            held.append(build_weights(sub.workload, sub.layers))
+            held.append(build_weights(sub.workload, sub.layers, sub.tp))
             held_key = key
         log(f"point {wl} M={m}")
         r = run_gemm(sub, held[0])
@@ -549,6 +574,9 @@ def main(argv=None) -> int:
     p.add_argument("--points", default="auto",
                    help="further workload:m points timed after the headline, comma-separated, or 'none' "
                         f"(auto: {DEFAULT_POINTS} when the headline is the default 70B M=1 sweep)")
+    p.add_argument("--tp", type=int, default=1,
+                   help="sweep one GPU's shard of a tensor-parallel layer: N/tp rows of q/k/v and gate/up, "
+                        "K/tp columns of o and down (the collectives are not part of this single-GPU build)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args(argv)
@@ -584,8 +612,9 @@ def main(argv=None) -> int:
         r = run_readsweep(args)
         metric = "plain device read GB/s over the llama3-70b sweep's launch sizes (weight-stream ceiling)"
         grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
-        workload = (f"read the packed IQ3_S bytes of llama3-70b's {args.layers} layers x 7 linears, one buffer "
-                    f"per launch, {grouping}")
+        shard = f" (one GPU's shard at tensor parallelism {args.tp})" if args.tp > 1 else ""
+        workload = (f"read the packed IQ3_S bytes of llama3-70b's {args.layers} layers x 7 linears{shard}, one "
+                    f"buffer per launch, {grouping}")
         config = {"workload": workload, "launches_per_step": r["launches"],
                   "bytes_gb": round(r["step_bytes"] / 1e9, 3), "graph": not args.no_graph}
         dtype, data = "u8", "uninitialised device bytes"
@@ -602,14 +631,14 @@ def main(argv=None) -> int:
         config = {"workload": workload, "m": 4096, "k": 4096}
         dtype, data = "bf16 -> fp8-e4m3 + e8m0", "synthetic (bf16 ~N(0,1), 0.1% x100 outliers)"
     else:
-        weights = build_weights(args.workload, args.layers)
+        weights = build_weights(args.workload, args.layers, args.tp)
         r = run_gemm(args, weights)
         metric = ("fused IQ3_S x MXFP8 GEMM TFLOP/s vs MX-FP8 MFMA roofline" if args.m >= PREFILL_M else
                   "fused IQ3_S x MXFP8 GEMM weight-stream GB/s vs HBM roofline")
         if args.with_quant != "none":
             metric += " (bf16 activations quantized in the step)"
         workload = gemm_workload_name(args)
-        config = {"workload": workload, "m": args.m, "projections_per_step": r["projections"],
+        config = {"workload": workload, "m": args.m, "tp_shard": args.tp, "projections_per_step": r["projections"],
                   "launches_per_step": r["launches"], "weight_gb": round(r["weight_bytes"] / 1e9, 3),
                   "tflops": round(r["tflops"], 3), "graph": not args.no_graph}
         held = [weights]  # sweep_points drops the headline weights before building others

@@ -7,7 +7,8 @@ oracle busy for minutes).
 * prefill on the four Llama-3-8B projection shapes at M = 2048 and 8192, with the
   library default and with the tuned table;
 * the Llama-3-70B sweep's seven projections at M = 1, 32 and 512, grouped into launches
-  as the benchmark groups them (q/k/v, o, gate/up, down);
+  as the benchmark groups them (q/k/v, o, gate/up, down), whole and as one GPU's shard of
+  an 8-way tensor-parallel layer (N/8 rows of q/k/v and gate/up, K/8 of o and down);
 * the reference's end-to-end check against the unquantized input
   (test_iq3_s_fp8.py:213-269) at M = 1, 4, 8, 128;
 * grouped launches through the tiled kernel's 16- and 32-token tiles.
@@ -32,6 +33,12 @@ LLAMA8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
 # Llama-3-70B layer: (name, N, K, input slot); projections of one slot share a launch
 LLAMA70B = [("q", 8192, 8192, 0), ("k", 1024, 8192, 0), ("v", 1024, 8192, 0), ("o", 8192, 8192, 1),
             ("gate", 28672, 8192, 2), ("up", 28672, 8192, 2), ("down", 8192, 28672, 3)]
+
+
+def tp_shard(layer: list, tp: int) -> list:
+    """One GPU's shard of a tp-way tensor-parallel layer: column-parallel projections
+    (input slots 0 and 2) keep N/tp rows, row-parallel ones (slots 1 and 3) K/tp columns."""
+    return [(name, n // tp, k, slot) if slot in (0, 2) else (name, n, k // tp, slot) for name, n, k, slot in layer]
 
 
 def sample_rows(n: int, count: int, seed: int) -> np.ndarray:
@@ -89,20 +96,22 @@ def test_prefill_llama8b_shapes(gpu, n, k, m):
         assert bool(torch.isfinite(out).all())
 
 
+@pytest.mark.parametrize("tp", [1, 8])
 @pytest.mark.parametrize("m", [1, 32, 512])
-def test_llama70b_layer_projections(gpu, m):
-    """One Llama-3-70B layer's seven projections in the benchmark's four launches (q/k/v
-    grouped, o, gate/up grouped, down) with the configurations it uses, sampled rows of
-    every projection against the oracle."""
+def test_llama70b_layer_projections(gpu, m, tp):
+    """One Llama-3-70B layer's seven projections (tp = 8: one GPU's shard of them) in the
+    benchmark's four launches (q/k/v grouped, o, gate/up grouped, down) with the
+    configurations it uses, sampled rows of every projection against the oracle."""
+    layer = tp_shard(LLAMA70B, tp)
     from mambo_amd.kernels.iq3_s_fp8 import (launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped,
                                              select_config)
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
     acts = {}
-    for _, _, k, slot in LLAMA70B:
+    for _, _, k, slot in layer:
         if slot not in acts:
             acts[slot] = launch_quantize_fp8(_synth_act(gpu, m, k, seed=200 + slot))
     weights = []
-    for j, (name, n, k, slot) in enumerate(LLAMA70B):
+    for j, (name, n, k, slot) in enumerate(layer):
         step(f"synth weight {name} {n}x{k}")
         weights.append((name, n, k, slot, 300 + j, _synth_weight(gpu, n, k, seed=300 + j)))
     for slot in range(4):
@@ -117,7 +126,7 @@ def test_llama70b_layer_projections(gpu, m):
             outs = launch_iq3_s_fp8_matmul_grouped(xv, xs, [w[5] for w in group], config=cfg)
         torch.cuda.synchronize()
         for (name, n, k, _, seed, _), out in zip(group, outs):
-            rows = sample_rows(n, 32 if m == 512 else 96, seed)
+            rows = sample_rows(n, min(n - 32, 32 if m == 512 else 96), seed)
             step(f"oracle {name} M={m} ({len(rows)} rows)")
             check(columns(out, rows), oracle_rows(xv, xs, seed, k, rows), elementwise=False)
 
