@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY. This file restates, in plain C, the arithmetic of
  * the reference path so that the HIP product can be checked against it. Only
  * tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py may load
- * the library built from it, and only as the checker or as the timed CPU
+ * the library built from it, and only to check results or as the timed CPU
  * baseline; the product (mambo_amd/) never links, imports or calls it.
  *
  * What each part follows (paths are in the Menooker/Mambo reference):

@@ -1,7 +1,8 @@
 """ctypes bindings for the CPU oracle in ``mambo_oracle.c``.
 
 Test infrastructure only: tests/, ``__graft_entry__.smoke()`` and the
-cpu_baseline leg of bench.py use it as the checker. The product package
+cpu_baseline leg of bench.py use it, to check results or as the timed CPU
+baseline. The product package
 (``mambo_amd``) never imports it.
 """
 
