@@ -125,7 +125,10 @@ int mambo_iq3s_dequant(const uint16_t *d, const uint32_t *qs, const uint16_t *qh
  * iq3_s_fp8_matmul / iq3_s_fp8_matmul_medium (iq3_s_fp8.py:225-333,364-399).
  * xv u8[m, ldxv] E4M3, xs u8[m, ldxs] E8M0 (K = blocks*256, K/32 scales per row);
  * packed: tile layout from mambo_iq3s_prepare/mambo_iq3s_pack.
- * xv and ldxv must be 16-byte aligned. cfg may be NULL (library default). When the
+ * xv and ldxv must be 16-byte aligned; configurations of the tiled kernel
+ * (MAMBO_GEMM_TILED, which the default picks from 17 tokens on) also need xs and ldxs
+ * 8-byte aligned and return MAMBO_ERR_VALUE otherwise (the stream and dense kernels take
+ * any xs). cfg may be NULL (library default). When the
  * chosen configuration splits K, `out` is zeroed on `stream` first and partial sums are
  * added with f32 atomics (results then vary in the last bits from run to run, as the
  * reference's split-K does). */
