@@ -1511,12 +1511,15 @@ __global__ __launch_bounds__(W * 64) void gemm_prefill_kernel(const uint8_t *__r
     }
 }
 
-// Zero row blockIdx.y of projection blockIdx.z's output (the split-K accumulators of
-// every projection of a launch in one dispatch). The projection is picked by selects
-// over constant indices, so the arguments stay in scalar registers.
-__global__ void zero_rows_kernel(GroupArgs ga)
+// Zero rows [0, M) of projection blockIdx.y's output (the split-K accumulators of every
+// projection of a launch in one dispatch): each thread clears a 4-float chunk of a row
+// (chunks flattened over rows, grid-strided), with one 16-byte store where the chunk is
+// whole and 16-byte aligned (column slices of a wider buffer may not be). The host keeps
+// M times the chunks per row below 2^31. The projection is picked by selects over
+// constant indices, so the arguments stay in scalar registers.
+__global__ __launch_bounds__(256) void zero_rows_kernel(GroupArgs ga, int M)
 {
-    const int g = blockIdx.z;
+    const int g = blockIdx.y;
     float *out = ga.out[0];
     int64_t cols = ga.n[0], ld = ga.ldo[0];
 #pragma unroll
@@ -1526,9 +1529,18 @@ __global__ void zero_rows_kernel(GroupArgs ga)
             cols = ga.n[i];
             ld = ga.ldo[i];
         }
-    const int64_t r = blockIdx.y;
-    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += (int64_t)gridDim.x * blockDim.x)
-        out[r * ld + c] = 0.0f;
+    const int chunks = (int)((cols + 3) / 4);
+    const int total = M * chunks;
+    for (int i = (int)blockIdx.x * 256 + (int)threadIdx.x; i < total; i += (int)gridDim.x * 256) {
+        const int r = i / chunks, c = 4 * (i - r * chunks);
+        float *p = out + r * ld + c;
+        if (c + 4 <= cols && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            __builtin_nontemporal_store(v4f{0.0f, 0.0f, 0.0f, 0.0f}, reinterpret_cast<v4f *>(p));
+        } else {
+            for (int j = c; j < cols && j < c + 4; ++j)
+                __builtin_nontemporal_store(0.0f, out + r * ld + j);
+        }
+    }
 }
 
 // Launch arguments of the stream kernel beyond the operands.
@@ -2205,8 +2217,10 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         int64_t n_max = 0;
         for (int g = 0; g < count; ++g)
             n_max = std::max(n_max, ga.n[g]);
-        dim3 zg((unsigned)std::min<int64_t>(cdiv(n_max, 256), 1024), (unsigned)m, (unsigned)count);
-        MAMBO_LAUNCH(zero_rows_kernel, zg, dim3(256), 0, s, ga);
+        const int64_t chunks = m * cdiv(n_max, 4); // 4-float chunks of the widest projection
+        MAMBO_REQUIRE(chunks <= 0x7FFFFFFF, MAMBO_ERR_VALUE, "output too large for one split-K launch");
+        dim3 zg((unsigned)std::min<int64_t>(cdiv(chunks, 256), 1024), (unsigned)count);
+        MAMBO_LAUNCH(zero_rows_kernel, zg, dim3(256), 0, s, ga, (int)m);
         rc = mambo_check_launch("zero_rows");
         if (rc)
             return rc;
