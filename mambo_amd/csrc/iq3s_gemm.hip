@@ -42,6 +42,45 @@ __device__ __align__(16) uint8_t g_zero_chunk[64] = {};
 __device__ uint8_t g_unit_scales[2] = {127, 127};
 __constant__ SplitTables c_split = kSplitTables;
 
+// The stream kernel's codebook in LDS holds 2^kLg copies of every E4M3 grid word: word
+// idx of copy c at dword (idx << kLg) + c, and lane l reads copy l mod 2^kLg. With 16
+// copies copy c lies in the banks c + 16j, so the 64 random lookups of an instruction
+// collide only within the 4 lanes that share a copy, where with one copy they all hash
+// into the same banks (one copy at M = 4 on 57344 x 8192: bank conflicts held the LDS
+// ~57% of its active time, SQ_LDS_BANK_CONFLICT against SQ_LDS_IDX_ACTIVE). More copies
+// cost LDS and so resident workgroups: stream_copies_lg picks the count per launch.
+// Each image is copied into LDS as it lies here (16-byte direct copies).
+template <int kLg>
+struct RepGrid {
+    uint32_t w[512 << kLg];
+};
+template <int kLg>
+constexpr RepGrid<kLg> make_rep_grid()
+{
+    RepGrid<kLg> r{};
+    for (int i = 0; i < (512 << kLg); ++i)
+        r.w[i] = kGridTables.fp8[i >> kLg];
+    return r;
+}
+__device__ __align__(16) const RepGrid<0> g_rep_grid0 = make_rep_grid<0>();
+__device__ __align__(16) const RepGrid<2> g_rep_grid2 = make_rep_grid<2>();
+__device__ __align__(16) const RepGrid<4> g_rep_grid4 = make_rep_grid<4>();
+
+template <int kLg>
+__device__ __forceinline__ const uint32_t *rep_grid()
+{
+    static_assert(kLg == 0 || kLg == 2 || kLg == 4, "built for 1, 4 and 16 codebook copies");
+    if constexpr (kLg == 0)
+        return g_rep_grid0.w;
+    else if constexpr (kLg == 2)
+        return g_rep_grid2.w;
+    else
+        return g_rep_grid4.w;
+}
+
+// LDS bytes of the codebook with 2^lg copies.
+__host__ __device__ constexpr int stream_lut_bytes(int lg) { return 2048 << lg; }
+
 // Super-blocks in flight per wave (register ring depth).
 #ifndef MAMBO_STREAM_DEPTH
 #define MAMBO_STREAM_DEPTH 2
@@ -117,6 +156,24 @@ __device__ __forceinline__ uint32_t code_addr(const uint32_t (&s)[5])
     }
 }
 
+// Byte address of code I's grid word in the codebook with 2^kLg copies, copy c4 / 4:
+// (idx << (kLg + 2)) + c4 (one shift or funnel shift and one and-or).
+template <int I, int kLg>
+__device__ __forceinline__ uint32_t rep_addr(const uint32_t (&s)[5], uint32_t c4)
+{
+    constexpr uint32_t kMask = 0x7FCu << kLg;
+    constexpr int p = 9 * I - 2 - kLg;
+    if constexpr (p < 0) {
+        return ((s[0] << (-p)) & kMask) | c4;
+    } else {
+        constexpr int wi = p >> 5, sh = p & 31;
+        if constexpr (wi + 1 <= 4)
+            return (funnel_shr(s[wi + 1], s[wi], sh) & kMask) | c4;
+        else
+            return ((s[wi] >> sh) & kMask) | c4;
+    }
+}
+
 // Signed E4M3 word of code C (0..7) of a group: grid magnitudes with the four sign
 // bits of the code moved onto bits 7, 15, 23, 31 by one rotate of the transposed word.
 template <int C>
@@ -126,12 +183,13 @@ __device__ __forceinline__ uint32_t signed_word(uint32_t mag, uint32_t p)
     return (rot & 0x80808080u) | mag;
 }
 
-template <int H, int... C>
-__device__ __forceinline__ v8i decode_group(const uint32_t (&s)[5], uint32_t p, const uint8_t *lut,
+// lut: the codebook with 2^kLg copies; c4: this lane's copy offset, 4 * (lane mod 2^kLg).
+template <int H, int kLg, int... C>
+__device__ __forceinline__ v8i decode_group(const uint32_t (&s)[5], uint32_t p, const uint8_t *lut, uint32_t c4,
                                             std::integer_sequence<int, C...>)
 {
     v8i b;
-    ((b[C] = (int)signed_word<C>(*reinterpret_cast<const uint32_t *>(lut + code_addr<8 * H + C>(s)), p)), ...);
+    ((b[C] = (int)signed_word<C>(*reinterpret_cast<const uint32_t *>(lut + rep_addr<8 * H + C, kLg>(s, c4)), p)), ...);
     return b;
 }
 
@@ -171,14 +229,14 @@ __device__ __forceinline__ void load_a(ATile<U> &at, const ALane (&al)[U], int b
     }
 }
 
-template <int U>
-__device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at, const uint8_t *lut, float (&acc)[U][4],
-                                              bool valid)
+template <int U, int kLg>
+__device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at, const uint8_t *lut, uint32_t c4,
+                                              float (&acc)[U][4], bool valid)
 {
     const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
     const float d = half_bits_to_float((uint16_t)w.dh);
-    const v8i b0 = decode_group<0>(s, w.sg.x, lut, std::make_integer_sequence<int, 8>{});
-    const v8i b1 = decode_group<1>(s, w.sg.y, lut, std::make_integer_sequence<int, 8>{});
+    const v8i b0 = decode_group<0, kLg>(s, w.sg.x, lut, c4, std::make_integer_sequence<int, 8>{});
+    const v8i b1 = decode_group<1, kLg>(s, w.sg.y, lut, c4, std::make_integer_sequence<int, 8>{});
     const uint32_t sc = w.sc;
     // A block past the wave's range (a duplicate of its last block) contributes nothing.
     const float f0 = valid ? d * (float)(1u + 2u * (sc & 15u)) : 0.0f;
@@ -345,7 +403,8 @@ __device__ __forceinline__ void stream_tile_end(float (&acc)[U][4], float *red, 
 // 2 f32; ldxv in elements) that the workgroup quantizes to MXFP8 into its LDS copy
 // itself (quantize_group32: the quantizer's arithmetic, so the codes are identical), in
 // place of a separate quantizer launch; xs is unused.
-template <int U, int W, bool kLdsAct, int kQ = 0>
+// kLg: log2 of the codebook copies in LDS (see RepGrid).
+template <int U, int W, bool kLdsAct, int kQ = 0, int kLg = 0>
 __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                              GroupArgs ga, int64_t ntiles, int tpw, int B, int bps,
@@ -372,15 +431,22 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
     // straight into LDS ahead of the ring's first weight loads: vector memory counts
     // complete in issue order, so the barrier below waits for the copies (L2) and not for
     // the weights (HBM), which stay in flight across it.
-    __shared__ uint32_t s_grid[512];
+    __shared__ __align__(16) uint32_t s_grid[512 << kLg];
     const uint8_t *lut = reinterpret_cast<const uint8_t *>(s_grid);
+    const uint32_t c4 = 4u * (uint32_t)(lane & ((1 << kLg) - 1));
     static_assert(kQ == 0 || kLdsAct, "quantizing rows needs the LDS copy");
     const int qgroups = rows * (K / 32); // kQ: 32-element groups to quantize
     float qv[32];
     {
-        const __amdgpu_buffer_rsrc_t gr = byte_rsrc(c_grid.fp8);
-        for (int i = wave; i < 8; i += W)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (lds_ptr)(s_grid + 64 * i), 4, 4u * lane, 256u * i, 0, 0);
+        const __amdgpu_buffer_rsrc_t gr = byte_rsrc(rep_grid<kLg>());
+        if constexpr (kLg == 0) { // one copy: 4-byte copies spread over up to 8 waves
+            for (int i = wave; i < 8; i += W)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (lds_ptr)(s_grid + 64 * i), 4, 4u * lane, 256u * i, 0, 0);
+        } else {
+            for (int i = wave; i < stream_lut_bytes(kLg) / 1024; i += W)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (lds_ptr)(s_grid + 256 * i), 16, 16u * lane, 1024u * i, 0,
+                                                         0);
+        }
         if constexpr (kQ != 0) {
             // the first group this thread quantizes: its loads go out before the ring's
             // weight loads, so waiting for them leaves the weights in flight
@@ -507,9 +573,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__re
                 const int blk = first + ci * W;
                 if constexpr (kLdsAct) {
                     load_a<U>(ar[0], al, min(blk, b_end - 1));
-                    compute_block<U>(wr[j], ar[0], lut, acc, blk < b_end);
+                    compute_block<U, kLg>(wr[j], ar[0], lut, c4, acc, blk < b_end);
                 } else {
-                    compute_block<U>(wr[j], ar[j], lut, acc, blk < b_end);
+                    compute_block<U, kLg>(wr[j], ar[j], lut, c4, acc, blk < b_end);
                 }
                 if (++ci == steps) {
                     stream_tile_end<U, W>(acc, red + (tile_no & 1) * (W * U * 64), wave, tid, lane,
@@ -1550,18 +1616,33 @@ struct StreamLaunch {
     int64_t ntiles; // 16-row tiles of the launch (all projections)
     int tpw;        // tiles per workgroup
     int B, bps, atomic;
+    int lg;         // log2 of the codebook copies (0, 2 or 4; 0 when U > 1 or quantizing)
 };
 
-template <int U, int W, bool kLdsAct, int kQ = 0>
+template <int U, int W, bool kLdsAct, int kQ = 0, int kLg = 0>
 void launch_stream_uwa(const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
                        int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
-    MAMBO_LAUNCH((gemm_stream_kernel<U, W, kLdsAct, kQ>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs,
+    MAMBO_LAUNCH((gemm_stream_kernel<U, W, kLdsAct, kQ, kLg>), sl.grid, dim3(W * 64), sl.lds, stream, xv, ldxv, xs,
                        ldxs, M, ga, sl.ntiles, sl.tpw, sl.B, sl.bps, sl.atomic);
 }
 
+template <int U, int W, bool kLdsAct>
+void launch_stream_uwl(const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
+                       int64_t ldxs, int64_t M, const GroupArgs &ga)
+{
+    if constexpr (U == 1) {
+        if (sl.lg == 2)
+            return launch_stream_uwa<U, W, kLdsAct, 0, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+        if (sl.lg == 4)
+            return launch_stream_uwa<U, W, kLdsAct, 0, 4>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+    }
+    launch_stream_uwa<U, W, kLdsAct>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+}
+
 // quant: -1 for MXFP8 activations, else the MAMBO_DTYPE_* of unquantized rows that the
-// kernel quantizes itself (built for one 4-token sub-tile with LDS-staged rows only).
+// kernel quantizes itself (built for one 4-token sub-tile with LDS-staged rows and one
+// codebook copy only).
 template <int U, int W>
 void launch_stream_uw(bool lds_act, int quant, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv,
                       int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
@@ -1573,9 +1654,9 @@ void launch_stream_uw(bool lds_act, int quant, const StreamLaunch &sl, hipStream
             return launch_stream_uwa<U, W, true, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
     }
     if (lds_act)
-        launch_stream_uwa<U, W, true>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+        launch_stream_uwl<U, W, true>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
     else
-        launch_stream_uwa<U, W, false>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+        launch_stream_uwl<U, W, false>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
 }
 
 // Waves per workgroup the stream kernel is built for.
@@ -1718,16 +1799,34 @@ constexpr int64_t kTiledMinM = 64;
 constexpr int kMaxDynLds = MAMBO_MAX_DYN_LDS_KB * 1024;
 // LDS per CU on gfx950.
 constexpr int kLdsPerCU = 160 * 1024;
+// Dynamic LDS a stream-kernel workgroup may take beside its static codebook of 2^lg copies.
+int stream_max_dyn_lds(int lg) { return kLdsPerCU - stream_lut_bytes(lg) - 1024; }
+
+// Codebook copies (log2) of a stream launch with `rows` tokens per workgroup over
+// `blocks` K blocks (graph-timed sweeps, one box): one copy for one token on K >= 8192
+// (70B M=1: 4 copies -0.2%, 16 copies -5%: the LDS they take costs resident
+// workgroups), 16 for 3-4 tokens on K >= 8192 (70B M=3 +4.7%, M=4 +8%), else 4 (70B M=2
+// +2.1%, 8B M=1 +1.0%, M=4 +2.2%). Several 4-token sub-tiles (M > 4) and in-kernel
+// quantization keep one copy.
+int stream_copies_lg(int64_t rows, int64_t blocks, int quant)
+{
+    if (quant >= 0 || rows > 4)
+        return 0;
+    if (blocks >= 32)
+        return rows == 1 ? 0 : rows >= 3 ? 4 : 2;
+    return 2;
+}
 
 // Whether the stream kernel stages its chunk's activations in LDS (`lds_bytes`: the
 // workgroup's whole dynamic LDS with them): when they take at most kMaxLdsAct, or when
-// the LDS still leaves room for 16 waves per CU (one 16-wave workgroup, two 8-wave ones).
+// the LDS (with the static codebook) still leaves room for 16 waves per CU (one 16-wave
+// workgroup, two 8-wave ones).
 // Beyond that they are read from L2 in the weight ring.
-bool stream_stages_act(int64_t act_bytes, int lds_bytes, int waves)
+bool stream_stages_act(int64_t act_bytes, int lds_bytes, int waves, int lg)
 {
-    if (lds_bytes > kMaxDynLds)
+    if (lds_bytes > stream_max_dyn_lds(lg))
         return false;
-    return act_bytes <= kMaxLdsAct || (int64_t)lds_bytes * 16 <= (int64_t)kLdsPerCU * waves;
+    return act_bytes <= kMaxLdsAct || (int64_t)(lds_bytes + stream_lut_bytes(lg)) * 16 <= (int64_t)kLdsPerCU * waves;
 }
 
 bool valid_waves(int w)
@@ -1869,7 +1968,8 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         // 8192 x 28672: 21.3 / 22.4 / 24.1 us at M = 2 / 3 / 4 against 26-28 us with them
         // read from L2 in the ring).
         const int64_t act = std::min<int64_t>(16, m) * blocks * 256 * 33 / 32;
-        if (act > kMaxLdsAct && blocks >= 32 && act + 8192 <= kMaxDynLds) {
+        if (act > kMaxLdsAct && blocks >= 32 &&
+            act + 8192 <= stream_max_dyn_lds(stream_copies_lg(std::min<int64_t>(16, m), blocks, -1))) {
             waves = 16;
             c.tile_n = (int32_t)(kTileRows * std::max<int64_t>(1, (units + kCUs / 2) / kCUs));
         }
@@ -2078,13 +2178,14 @@ int plan_streaming(const mambo_gemm_config &c, const uint8_t *xv, int64_t ldxv, 
         return MAMBO_OK;
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
+        const int lg = stream_copies_lg(rows, blocks, quant);
         lds_act = stream_stages_act((int64_t)rows * k * 33 / 32,
-                                    stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves);
+                                    stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves, lg);
         // the staging copies move activation scales as dwords
         if (quant < 0 && ((uintptr_t)xs % 4 != 0 || ldxs % 4 != 0))
             lds_act = false;
         const StreamLds L = stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, lds_act);
-        MAMBO_REQUIRE(L.total <= kMaxDynLds, MAMBO_ERR_VALUE,
+        MAMBO_REQUIRE(L.total <= stream_max_dyn_lds(lg), MAMBO_ERR_VALUE,
                       "configuration needs %d bytes of LDS per workgroup (waves=%d, M=%lld); use fewer waves", L.total,
                       c.waves, (long long)m);
         int64_t runs = c.tile_n ? c.tile_n / kTileRows : 1;
@@ -2093,7 +2194,7 @@ int plan_streaming(const mambo_gemm_config &c, const uint8_t *xv, int64_t ldxv, 
         if (quant >= 0)
             runs = std::max<int64_t>(runs, cdiv(tiles, kFusedWgs));
         const int tpw = (int)std::min<int64_t>(runs, tiles);
-        StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic};
+        StreamLaunch sl = {grid, (size_t)L.total, tiles, tpw, B, bps, atomic, lg};
         sl.grid.x = (unsigned)cdiv(tiles, tpw);
         const int waves = c.waves;
         launch = [=](bool dry) {
@@ -2171,7 +2272,7 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         const int qrows = (int)std::min<int64_t>(4, m);
         const int qlds = stream_lds(1, c.waves, qrows, (int)k, true).total;
         if (c.kernel != MAMBO_GEMM_STREAM || m > 4 || (uintptr_t)xv % 16 != 0 || (ldxv * esz) % 16 != 0 ||
-            !stream_stages_act((int64_t)qrows * k * 33 / 32, qlds, c.waves) || qlds > kMaxDynLds)
+            !stream_stages_act((int64_t)qrows * k * 33 / 32, qlds, c.waves, 0) || qlds > stream_max_dyn_lds(0))
             return kNotFused;
     }
     const int bps = (int)cdiv(blocks, c.split_k);

@@ -293,6 +293,38 @@ def test_stream_kernel_multi_tile_runs(gpu, m):
                         np.testing.assert_array_equal(o, b)
 
 
+@pytest.mark.parametrize("k", [2048, 8192])
+def test_stream_kernel_codebook_copies(gpu, k):
+    """The stream kernel keeps 1, 4 or 16 copies of its codebook in LDS, chosen by the
+    launch's tokens and K (1 token on K >= 8192: one copy; 2 tokens: four; 3-4 tokens on
+    K >= 8192: sixteen; K < 8192: four). Every token count against the oracle, for 1, 4
+    and 16 waves with runs of tiles; and each token's outputs bit for bit equal to a
+    one-token launch of that token (the block-diagonal MFMA computes every token's
+    outputs alone, so only a wrong codebook word could change them)."""
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n = 200
+    raw = make_synthetic_iq3_s(n, k, seed=k + 7)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    x = np.random.default_rng(k).standard_normal((4, k)).astype(np.float32)
+    xv, xs = oracle.quantize_mxfp8(x)
+    xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+    expected = oracle.iq3s_fp8_matmul(xv, xs, raw)
+    for waves, tiles_per_wg in ((1, 1), (4, 1), (4, 3), (16, 2)):
+        cfg = {"kernel": _native.GEMM_STREAM, "waves": waves, "split_k": 1, "tile_n": 16 * tiles_per_wg}
+        single = []
+        for t in range(4):
+            step(f"stream codebook copies: token {t} alone K={k} cfg={cfg}")
+            single.append(launch_iq3_s_fp8_matmul(xvg[t:t + 1], xsg[t:t + 1], fields, config=cfg).cpu().numpy())
+        for m in (1, 2, 3, 4):
+            step(f"stream codebook copies: M={m} K={k} cfg={cfg}")
+            out = launch_iq3_s_fp8_matmul(xvg[:m], xsg[:m], fields, config=cfg).cpu().numpy()
+            check(out, expected[:m])
+            for t in range(m):
+                np.testing.assert_array_equal(out[t:t + 1], single[t], err_msg=f"token {t} of M={m}")
+
+
 def test_grouped_into_strided_outputs(gpu):
     from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul_grouped
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
