@@ -193,6 +193,51 @@ __device__ __forceinline__ v8i decode_group(const uint32_t (&s)[5], uint32_t p, 
     return b;
 }
 
+// Codebook reads of a tile-block in batches of kB (16 codes per lane): batch k+1's reads
+// are issued before batch k's words are used (sched_barrier fences keep the order), so
+// the waits before the sign operations are partial and up to 2kB reads are in flight.
+// The compiler's own order pairs each read with its use, waiting for every read: 16 LDS
+// round trips per step in series, which the last step of each workgroup exposes at the
+// end of a launch. One copy (M = 1), batches of 4: 70B M=1 sweep +1.1%, 8B +0.9% (2: +0.9
+// / +0.4%, 8: +0.8 / -0.2%, 80 VGPRs); with 4 or 16 copies (M = 2..4) no gain.
+template <int kLg, int I0, int N>
+__device__ __forceinline__ void fetch_codes(const uint32_t (&s)[5], const uint8_t *lut, uint32_t c4,
+                                            uint32_t (&mag)[16])
+{
+    if constexpr (N > 0) {
+        mag[I0] = *reinterpret_cast<const uint32_t *>(lut + rep_addr<I0, kLg>(s, c4));
+        fetch_codes<kLg, I0 + 1, N - 1>(s, lut, c4, mag);
+    }
+}
+template <int I0, int N>
+__device__ __forceinline__ void sign_codes(const uint32_t (&mag)[16], uint32_t p0, uint32_t p1, v8i &b0, v8i &b1)
+{
+    if constexpr (N > 0) {
+        constexpr int C = I0 % 8;
+        if constexpr (I0 < 8)
+            b0[C] = (int)signed_word<C>(mag[I0], p0);
+        else
+            b1[C] = (int)signed_word<C>(mag[I0], p1);
+        sign_codes<I0 + 1, N - 1>(mag, p0, p1, b0, b1);
+    }
+}
+template <int kLg, int kB, int K = 0>
+__device__ __forceinline__ void decode_batched(const uint32_t (&s)[5], uint32_t p0, uint32_t p1, const uint8_t *lut,
+                                               uint32_t c4, uint32_t (&mag)[16], v8i &b0, v8i &b1)
+{
+    static_assert(16 % kB == 0, "batches must cover the 16 codes");
+    if constexpr (K == 0)
+        fetch_codes<kLg, 0, kB>(s, lut, c4, mag);
+    if constexpr ((K + 1) * kB < 16) {
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_codes<kLg, (K + 1) * kB, kB>(s, lut, c4, mag);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    sign_codes<K * kB, kB>(mag, p0, p1, b0, b1);
+    if constexpr ((K + 1) * kB < 16)
+        decode_batched<kLg, kB, K + 1>(s, p0, p1, lut, c4, mag, b0, b1);
+}
+
 template <int U>
 struct ATile {
     v8i a[U][2];
@@ -235,8 +280,14 @@ __device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at
 {
     const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
     const float d = half_bits_to_float((uint16_t)w.dh);
-    const v8i b0 = decode_group<0, kLg>(s, w.sg.x, lut, c4, std::make_integer_sequence<int, 8>{});
-    const v8i b1 = decode_group<1, kLg>(s, w.sg.y, lut, c4, std::make_integer_sequence<int, 8>{});
+    v8i b0, b1;
+    if constexpr (kLg == 0) {
+        uint32_t mag[16];
+        decode_batched<kLg, 4>(s, w.sg.x, w.sg.y, lut, c4, mag, b0, b1);
+    } else {
+        b0 = decode_group<0, kLg>(s, w.sg.x, lut, c4, std::make_integer_sequence<int, 8>{});
+        b1 = decode_group<1, kLg>(s, w.sg.y, lut, c4, std::make_integer_sequence<int, 8>{});
+    }
     const uint32_t sc = w.sc;
     // A block past the wave's range (a duplicate of its last block) contributes nothing.
     const float f0 = valid ? d * (float)(1u + 2u * (sc & 15u)) : 0.0f;
