@@ -1678,31 +1678,30 @@ void launch_stream_uwa(const StreamLaunch &sl, hipStream_t stream, const uint8_t
                        ldxs, M, ga, sl.ntiles, sl.tpw, sl.B, sl.bps, sl.atomic);
 }
 
-template <int U, int W, bool kLdsAct>
+template <int U, int W, bool kLdsAct, int kQ = 0>
 void launch_stream_uwl(const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs,
                        int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
     if constexpr (U == 1) {
         if (sl.lg == 2)
-            return launch_stream_uwa<U, W, kLdsAct, 0, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+            return launch_stream_uwa<U, W, kLdsAct, kQ, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
         if (sl.lg == 4)
-            return launch_stream_uwa<U, W, kLdsAct, 0, 4>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+            return launch_stream_uwa<U, W, kLdsAct, kQ, 4>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
     }
-    launch_stream_uwa<U, W, kLdsAct>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+    launch_stream_uwa<U, W, kLdsAct, kQ>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
 }
 
 // quant: -1 for MXFP8 activations, else the MAMBO_DTYPE_* of unquantized rows that the
-// kernel quantizes itself (built for one 4-token sub-tile with LDS-staged rows and one
-// codebook copy only).
+// kernel quantizes itself (built for one 4-token sub-tile with LDS-staged rows only).
 template <int U, int W>
 void launch_stream_uw(bool lds_act, int quant, const StreamLaunch &sl, hipStream_t stream, const uint8_t *xv,
                       int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga)
 {
     if constexpr (U == 1) {
         if (quant == MAMBO_DTYPE_BF16)
-            return launch_stream_uwa<U, W, true, 1>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+            return launch_stream_uwl<U, W, true, 1>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
         if (quant == MAMBO_DTYPE_F32)
-            return launch_stream_uwa<U, W, true, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
+            return launch_stream_uwl<U, W, true, 2>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
     }
     if (lds_act)
         launch_stream_uwl<U, W, true>(sl, stream, xv, ldxv, xs, ldxs, M, ga);
@@ -1857,11 +1856,10 @@ int stream_max_dyn_lds(int lg) { return kLdsPerCU - stream_lut_bytes(lg) - 1024;
 // `blocks` K blocks (graph-timed sweeps, one box): one copy for one token on K >= 8192
 // (70B M=1: 4 copies -0.2%, 16 copies -5%: the LDS they take costs resident
 // workgroups), 16 for 3-4 tokens on K >= 8192 (70B M=3 +4.7%, M=4 +8%), else 4 (70B M=2
-// +2.1%, 8B M=1 +1.0%, M=4 +2.2%). Several 4-token sub-tiles (M > 4) and in-kernel
-// quantization keep one copy.
-int stream_copies_lg(int64_t rows, int64_t blocks, int quant)
+// +2.1%, 8B M=1 +1.0%, M=4 +2.2%). Several 4-token sub-tiles (M > 4) keep one copy.
+int stream_copies_lg(int64_t rows, int64_t blocks)
 {
-    if (quant >= 0 || rows > 4)
+    if (rows > 4)
         return 0;
     if (blocks >= 32)
         return rows == 1 ? 0 : rows >= 3 ? 4 : 2;
@@ -2020,7 +2018,7 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
         // read from L2 in the ring).
         const int64_t act = std::min<int64_t>(16, m) * blocks * 256 * 33 / 32;
         if (act > kMaxLdsAct && blocks >= 32 &&
-            act + 8192 <= stream_max_dyn_lds(stream_copies_lg(std::min<int64_t>(16, m), blocks, -1))) {
+            act + 8192 <= stream_max_dyn_lds(stream_copies_lg(std::min<int64_t>(16, m), blocks))) {
             waves = 16;
             c.tile_n = (int32_t)(kTileRows * std::max<int64_t>(1, (units + kCUs / 2) / kCUs));
         }
@@ -2229,7 +2227,7 @@ int plan_streaming(const mambo_gemm_config &c, const uint8_t *xv, int64_t ldxv, 
         return MAMBO_OK;
     } else {
         const int U = (int)std::min<int64_t>(4, cdiv(m, 4));
-        const int lg = stream_copies_lg(rows, blocks, quant);
+        const int lg = stream_copies_lg(rows, blocks);
         lds_act = stream_stages_act((int64_t)rows * k * 33 / 32,
                                     stream_lds(U, c.waves, std::min(rows, 4 * U), (int)k, true).total, c.waves, lg);
         // the staging copies move activation scales as dwords
@@ -2322,8 +2320,9 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         const int64_t esz = quant == MAMBO_DTYPE_BF16 ? 2 : 4;
         const int qrows = (int)std::min<int64_t>(4, m);
         const int qlds = stream_lds(1, c.waves, qrows, (int)k, true).total;
+        const int qlg = stream_copies_lg(qrows, blocks);
         if (c.kernel != MAMBO_GEMM_STREAM || m > 4 || (uintptr_t)xv % 16 != 0 || (ldxv * esz) % 16 != 0 ||
-            !stream_stages_act((int64_t)qrows * k * 33 / 32, qlds, c.waves, 0) || qlds > stream_max_dyn_lds(0))
+            !stream_stages_act((int64_t)qrows * k * 33 / 32, qlds, c.waves, qlg) || qlds > stream_max_dyn_lds(qlg))
             return kNotFused;
     }
     const int bps = (int)cdiv(blocks, c.split_k);
