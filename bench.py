@@ -24,7 +24,7 @@ linear N=K=4096 with M=8, timed on this host.
 
     python bench.py [--steps K] [--warmup W] [--m M]
                     [--workload llama70b|llama8b|quant|copy|read|readsweep|mfma]
-                    [--layers L] [--tp G] [--no-group] [--no-graph] [--with-quant none|separate|fused]
+                    [--model llama70b|llama8b] [--layers L] [--tp G] [--no-group] [--no-graph] [--with-quant none|separate|fused]
 """
 
 from __future__ import annotations
@@ -84,7 +84,7 @@ def layer_shapes(workload: str, tp: int = 1) -> list:
     tensor-parallel layer: the column-parallel projections (q/k/v, gate/up: slots 0 and 2)
     keep N/tp rows, the row-parallel ones (o, down: slots 1 and 3) K/tp columns, whole
     256-weight blocks (their partial outputs would be summed across GPUs)."""
-    shapes = LLAMA70B_LAYER if workload in ("llama70b", "readsweep") else LLAMA8B_LAYER
+    shapes = LLAMA70B_LAYER if workload == "llama70b" else LLAMA8B_LAYER
     if tp == 1:
         return shapes
     out = []
@@ -380,7 +380,7 @@ def run_read(args):
 def sweep_launch_bytes(args) -> list:
     """Packed IQ3_S bytes each launch of the projection sweep reads (the grouping of
     build_gemm_workload: q/k/v and gate/up share a launch unless args.no_group)."""
-    shapes = layer_shapes(args.workload, args.tp)
+    shapes = layer_shapes(args.model, args.tp)
     sizes = []
     for _ in range(args.layers):
         prev = None
@@ -395,7 +395,7 @@ def sweep_launch_bytes(args) -> list:
 
 
 def run_readsweep(args):
-    """Plain read (mambo_read_bytes) of one buffer per launch of the Llama-3-70B sweep, each
+    """Plain read (mambo_read_bytes) of one buffer per launch of the --model sweep, each
     the size of the packed weights that launch streams, replayed from a HIP graph: the
     ceiling a weight stream with this launch structure can reach on this device (per-launch
     ramp-up and drain included). The last buffer's read is checked against its XOR."""
@@ -564,6 +564,9 @@ def main(argv=None) -> int:
     p.add_argument("--workload", choices=["llama70b", "llama8b", "quant", "copy", "read", "readsweep", "mfma"],
                    default="llama70b")
     p.add_argument("--layers", type=int, default=None, help="layers in the sweep (default 80 for llama70b, 32 for llama8b)")
+    p.add_argument("--model", choices=["llama70b", "llama8b"], default=None,
+                   help="the sweep whose launch sizes --workload readsweep reads (default llama70b; the GEMM "
+                        "workloads name their model themselves)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--with-quant", choices=["none", "separate", "fused"], default="none",
                    help="time the activation quantization in the step: a quantizer launch before each GEMM "
@@ -580,8 +583,10 @@ def main(argv=None) -> int:
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args(argv)
+    if args.model is None:
+        args.model = args.workload if args.workload in ("llama70b", "llama8b") else "llama70b"
     if args.layers is None:
-        args.layers = 32 if args.workload == "llama8b" else 80
+        args.layers = 32 if args.model == "llama8b" else 80
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -610,10 +615,11 @@ def main(argv=None) -> int:
         dtype, data = "u8", "synthetic bytes"
     elif args.workload == "readsweep":
         r = run_readsweep(args)
-        metric = "plain device read GB/s over the llama3-70b sweep's launch sizes (weight-stream ceiling)"
+        model = "llama3-8b" if args.model == "llama8b" else "llama3-70b"
+        metric = f"plain device read GB/s over the {model} sweep's launch sizes (weight-stream ceiling)"
         grouping = "one launch per projection" if args.no_group else "q/k/v and gate/up grouped per launch"
         shard = f" (one GPU's shard at tensor parallelism {args.tp})" if args.tp > 1 else ""
-        workload = (f"read the packed IQ3_S bytes of llama3-70b's {args.layers} layers x 7 linears{shard}, one "
+        workload = (f"read the packed IQ3_S bytes of {model}'s {args.layers} layers x 7 linears{shard}, one "
                     f"buffer per launch, {grouping}")
         config = {"workload": workload, "launches_per_step": r["launches"],
                   "bytes_gb": round(r["step_bytes"] / 1e9, 3), "graph": not args.no_graph}
