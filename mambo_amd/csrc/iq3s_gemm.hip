@@ -46,7 +46,7 @@ __constant__ SplitTables c_split = kSplitTables;
 // idx of copy c at dword (idx << kLg) + c, and lane l reads copy l mod 2^kLg. With 16
 // copies copy c lies in the banks c + 16j, so the 64 random lookups of an instruction
 // collide only within the 4 lanes that share a copy, where with one copy they all hash
-// into the same banks (one copy at M = 4 on 57344 x 8192: bank conflicts held the LDS
+// into the same banks (one copy at M = 1 on 57344 x 8192: bank conflicts held the LDS
 // ~57% of its active time, SQ_LDS_BANK_CONFLICT against SQ_LDS_IDX_ACTIVE). More copies
 // cost LDS and so resident workgroups: stream_copies_lg picks the count per launch.
 // Each image is copied into LDS as it lies here (16-byte direct copies).
@@ -1856,7 +1856,8 @@ int stream_max_dyn_lds(int lg) { return kLdsPerCU - stream_lut_bytes(lg) - 1024;
 // `blocks` K blocks (graph-timed sweeps, one box): one copy for one token on K >= 8192
 // (70B M=1: 4 copies -0.2%, 16 copies -5%: the LDS they take costs resident
 // workgroups), 16 for 3-4 tokens on K >= 8192 (70B M=3 +4.7%, M=4 +8%), else 4 (70B M=2
-// +2.1%, 8B M=1 +1.0%, M=4 +2.2%). Several 4-token sub-tiles (M > 4) keep one copy.
+// +2.1%, 8B M=1 +1.0%, M=4 +2.2%). Several 4-token sub-tiles (M > 4) keep one copy (4
+// copies for 5-8 tokens on K = 4096: 8B M=8 sweep -3%).
 int stream_copies_lg(int64_t rows, int64_t blocks)
 {
     if (rows > 4)
