@@ -382,6 +382,19 @@ __device__ __forceinline__ void advance(StreamCursor &c, int total, int steps, c
     }
 }
 
+// Sum of a value over the four 16-lane groups, in every lane: v + v[l^16], then + [l^32],
+// by row swaps in the VALU (v_permlane16_swap / v_permlane32_swap) instead of LDS
+// permutes; a + b is commutative, so every lane gets the bits of the shuffle form.
+__device__ __forceinline__ float lane_group_sum(float v)
+{
+    const uint32_t x = __float_as_uint(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    const float s16 = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const uint32_t y = __float_as_uint(s16);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(y, y, false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
 // End of a tile: sum the wave's four K chunks (lane groups), then the waves' sums through
 // LDS, store (or add, when K is split over workgroups) the 16 x 4U outputs, clear acc.
 template <int U, int W>
@@ -393,8 +406,7 @@ __device__ __forceinline__ void stream_tile_end(float (&acc)[U][4], float *red, 
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             float v = acc[u][k];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
+            v = lane_group_sum(v);
             acc[u][k] = v;
         }
     if constexpr (W == 1) {
