@@ -49,7 +49,8 @@ __constant__ SplitTables c_split = kSplitTables;
 // into the same banks (one copy at M = 1 on 57344 x 8192: bank conflicts held the LDS
 // ~57% of its active time, SQ_LDS_BANK_CONFLICT against SQ_LDS_IDX_ACTIVE). More copies
 // cost LDS and so resident workgroups: stream_copies_lg picks the count per launch.
-// Each image is copied into LDS as it lies here (16-byte direct copies).
+// Each image is copied into LDS as it lies here (direct copies: 16-byte, 4-byte for one
+// copy).
 template <int kLg>
 struct RepGrid {
     uint32_t w[512 << kLg];
@@ -1679,7 +1680,7 @@ struct StreamLaunch {
     int64_t ntiles; // 16-row tiles of the launch (all projections)
     int tpw;        // tiles per workgroup
     int B, bps, atomic;
-    int lg;         // log2 of the codebook copies (0, 2 or 4; 0 when U > 1 or quantizing)
+    int lg;         // log2 of the codebook copies (0, 2 or 4; 0 when U > 1)
 };
 
 template <int U, int W, bool kLdsAct, int kQ = 0, int kLg = 0>
