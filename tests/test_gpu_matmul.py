@@ -88,6 +88,30 @@ def test_every_search_space_config_agrees(gpu):
             check(out.cpu().numpy(), expected)
 
 
+def test_every_stream_config_at_long_k(gpu):
+    """Every stream-kernel candidate at K=8192, where 1, 2 and 4 tokens take one, four and
+    sixteen codebook copies in LDS (every wave count, run length and K split of the
+    search space), against the oracle."""
+    from mambo_amd import _native
+    from mambo_amd.kernels.iq3_s_fp8 import gemm_search_space, launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    n_rows, k = 48, 8192
+    raw = make_synthetic_iq3_s(n_rows, k, seed=23)
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    for m in (1, 2, 4):
+        x = np.random.default_rng(100 + m).standard_normal((m, k)).astype(np.float32)
+        xv, xs = oracle.quantize_mxfp8(x)
+        expected = oracle.iq3s_fp8_matmul(xv, xs, raw)
+        xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+        cfgs = [c for c in gemm_search_space(m, n_rows, k) if c["kernel"] == _native.GEMM_STREAM]
+        assert cfgs
+        for cfg in cfgs:
+            step(f"stream M={m} N=48 K=8192 cfg={cfg}")
+            out = launch_iq3_s_fp8_matmul(xvg, xsg, fields, config=cfg)
+            torch.cuda.synchronize()
+            check(out.cpu().numpy(), expected, elementwise=False)
+
+
 def test_output_row_stride_and_preallocated_out(gpu):
     from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
