@@ -43,10 +43,8 @@ HBM_PEAK_GBS = 8000.0
 MXFP8_PEAK_TFLOPS = 5000.0  # dense MX-FP8 MFMA peak of MI355X
 PREFILL_M = 128  # from this many tokens the projections are MFMA-bound: report TFLOP/s
 
-LLAMA70B_LAYER = [("q", 8192, 8192, 0), ("k", 1024, 8192, 0), ("v", 1024, 8192, 0), ("o", 8192, 8192, 1),
-                  ("gate", 28672, 8192, 2), ("up", 28672, 8192, 2), ("down", 8192, 28672, 3)]
-LLAMA8B_LAYER = [("q", 4096, 4096, 0), ("k", 1024, 4096, 0), ("v", 1024, 4096, 0), ("o", 4096, 4096, 1),
-                 ("gate", 14336, 4096, 2), ("up", 14336, 4096, 2), ("down", 4096, 14336, 3)]
+from mambo_amd.utils.sweep import (build_launches, build_weights, capture, launch_shape, layer_shapes,  # noqa: E402
+                                   make_step, time_replays)
 
 
 def log(msg: str) -> None:
@@ -57,98 +55,15 @@ def proj_bytes(m: int, n: int, k: int, act_bytes_per_value: float = 33 / 32) -> 
     return n * k * 110 // 256 + int(m * k * act_bytes_per_value) + 4 * m * n
 
 
-def synth_weight(n: int, k: int, seed: int):
-    import torch
-    from mambo_amd import _native
-    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
-    raw = torch.empty((n, k // 256, 110), dtype=torch.uint8, device="cuda")
-    _native.check(_native.lib().mambo_synth_iq3s(seed, k // 256, 0, n, raw.data_ptr(), _native.stream_handle(None)))
-    fields = prepare_iq3_s_fields(raw, fields=False)
-    del raw
-    return fields
-
-
-def synth_activation(m: int, k: int, seed: int):
-    """(E4M3 values, E8M0 scales, bf16 rows) of synthetic ~N(0,1) activations."""
-    import torch
-    from mambo_amd import _native
-    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
-    bits = torch.empty(m * k, dtype=torch.int16, device="cuda")
-    _native.check(_native.lib().mambo_synth_bf16(seed, 2, 0.0, 0, m * k, bits.data_ptr(), _native.stream_handle(None)))
-    rows = bits.view(torch.bfloat16).view(m, k)
-    return (*launch_quantize_fp8(rows), rows)
-
-
-def layer_shapes(workload: str, tp: int = 1) -> list:
-    """(name, N, K, input slot) of one layer's linears; with tp > 1, one GPU's shard of a
-    tensor-parallel layer: the column-parallel projections (q/k/v, gate/up: slots 0 and 2)
-    keep N/tp rows, the row-parallel ones (o, down: slots 1 and 3) K/tp columns, whole
-    256-weight blocks (their partial outputs would be summed across GPUs)."""
-    shapes = LLAMA70B_LAYER if workload == "llama70b" else LLAMA8B_LAYER
-    if tp == 1:
-        return shapes
-    out = []
-    for name, n, k, slot in shapes:
-        if slot in (0, 2):
-            if n % (16 * tp):
-                raise ValueError(f"{name}: N={n} does not split into {tp} shards of whole 16-row tiles")
-            out.append((name, n // tp, k, slot))
-        else:
-            if k % (256 * tp):
-                raise ValueError(f"{name}: K={k} does not split into {tp} shards of whole 256-weight blocks")
-            out.append((name, n, k // tp, slot))
-    return out
-
-
-def build_weights(workload: str, layers: int, tp: int = 1):
-    """The sweep's distinct IQ3_S weights (packed form only), generated on the GPU:
-    [(layer, name, n, k, slot, fields)], seed 1000*layer + index in the layer."""
-    import torch
-    shapes = layer_shapes(workload, tp)
-    weights = []
-    t0 = time.time()
-    for layer in range(layers):
-        for j, (name, n, k, slot) in enumerate(shapes):
-            weights.append((layer, name, n, k, slot, synth_weight(n, k, seed=1000 * layer + j)))
-        if layer % 10 == 9:
-            log(f"prepared {layer + 1}/{layers} layers ({time.time() - t0:.1f} s)")
-    torch.cuda.synchronize()
-    return weights
-
-
-def build_launches(weights, m: int, no_group: bool):
-    """Activations, outputs and the launch list of one step at m tokens. Each launch is
-    (names, [(n, k, fields, out)], (x_values, x_scales, bf16 rows)); projections of one
-    layer that read the same input (q/k/v, gate/up) share a launch unless no_group."""
-    import torch
-    acts, outs, launches = {}, {}, []
-    for layer, name, n, k, slot, fields in weights:
-        if slot not in acts:
-            acts[slot] = synth_activation(m, k, seed=1 + slot)
-        key = (name, n, k)
-        if key not in outs:
-            outs[key] = torch.empty((m, n), dtype=torch.float32, device="cuda")
-        proj = (n, k, fields, outs[key])
-        if not no_group and launches and launches[-1][3] == (layer, slot) and len(launches[-1][1]) < 4:
-            launches[-1][0].append(name)
-            launches[-1][1].append(proj)
-        else:
-            launches.append(([name], [proj], acts[slot], (layer, slot)))
-    torch.cuda.synchronize()
-    return [(names, projs, act) for names, projs, act, _ in launches]
-
-
 def run_gemm(args, weights=None):
     import torch
-    from mambo_amd.kernels.iq3_s_fp8 import (launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped,
-                                             launch_iq3_s_matmul_quantize, select_config)
-    from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+    from mambo_amd.kernels.iq3_s_fp8 import select_config
 
     if weights is None:
         weights = build_weights(args.workload, args.layers, args.tp)
     launches = build_launches(weights, args.m, args.no_group)
     projections = [p for (_, projs, _) in launches for p in projs]
-    configs = [select_config(args.m, sum(n for n, _, _, _ in projs), projs[0][1]) for (_, projs, _) in launches]
+    configs = [select_config(args.m, *launch_shape(projs)) for (_, projs, _) in launches]
     weight_bytes = sum(f.packed.numel() for (_, _, f, _) in projections)
     # with quantization in the step the activations come in as bf16 rows
     act_bytes = 2 if args.with_quant != "none" else 33 / 32
@@ -157,34 +72,15 @@ def run_gemm(args, weights=None):
     log(f"{len(projections)} projections in {len(launches)} launches, {weight_bytes / 1e9:.2f} GB of IQ3_S "
         "weights resident")
 
-    def step():
-        for (_, projs, (xv, xs, rows)), cfg in zip(launches, configs):
-            if args.with_quant == "fused":
-                launch_iq3_s_matmul_quantize(rows, [p[2] for p in projs], config=cfg, outs=[p[3] for p in projs])
-                continue
-            if args.with_quant == "separate":
-                launch_quantize_fp8(rows, out=(xv, xs))
-            if len(projs) == 1:
-                launch_iq3_s_fp8_matmul(xv, xs, projs[0][2], config=cfg, out=projs[0][3])
-            else:
-                launch_iq3_s_fp8_matmul_grouped(xv, xs, [p[2] for p in projs], config=cfg,
-                                                outs=[p[3] for p in projs])
-
+    step = make_step(launches, configs, args.with_quant)
     outputs = list({id(o): o for (_, _, _, o) in projections}.values())
-    stream = torch.cuda.current_stream()
     step()
     torch.cuda.synchronize()
     replay = step
     if not args.no_graph:
         # Capture one step on a side stream, then check one replay against eager results.
         ref = [o.clone() for o in outputs]
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(graph, stream=side):
-                step()
-        stream.wait_stream(side)
+        graph = capture(step)
         for o in outputs:
             o.fill_(float("nan"))
         graph.replay()
@@ -199,19 +95,7 @@ def run_gemm(args, weights=None):
         replay = graph.replay
         log("captured the step in a HIP graph; replay matches eager")
 
-    for _ in range(args.warmup):
-        replay()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        replay()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = start.elapsed_time(stop) / args.steps
+    ms, wall = time_replays(replay, args.steps, args.warmup)
     gbs = step_bytes / (ms * 1e-3) / 1e9
     tflops = step_flops / (ms * 1e-3) / 1e12
     log(f"{ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), {gbs:.1f} GB/s, {tflops:.2f} TFLOP/s")
@@ -379,7 +263,7 @@ def run_read(args):
 
 def sweep_launch_bytes(args) -> list:
     """Packed IQ3_S bytes each launch of the projection sweep reads (the grouping of
-    build_gemm_workload: q/k/v and gate/up share a launch unless args.no_group)."""
+    mambo_amd.utils.sweep.build_launches: q/k/v and gate/up share a launch unless args.no_group)."""
     shapes = layer_shapes(args.model, args.tp)
     sizes = []
     for _ in range(args.layers):

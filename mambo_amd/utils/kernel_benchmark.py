@@ -14,6 +14,10 @@ of the candidates; a tuned entry replaces it only when it is faster by ``min_gai
 
     python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --model M.gguf --weight-name NAME
     python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --synthetic 4096 4096 [--write-table]
+    python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --sweep llama70b --tokens 1 16 [--write-table]
+
+``--sweep`` tunes every launch shape of a Llama-3 projection sweep inside the sweep
+itself, replayed from a HIP graph, where the step time decides (sweep_tune).
 
 The reference copies winners into BEST_CONFIGS by hand (kernels/AGENTS.md:27); here
 ``--write-table`` stores them per shape in mambo_amd/kernels/tuned_gfx950.json, which
@@ -218,6 +222,99 @@ def write_tuned_table(results: Sequence[TuneResult], path: Path, arch: str) -> N
     path.write_text(json.dumps(table, indent=1, sort_keys=True) + "\n")
 
 
+def _rel_l2(out: torch.Tensor, ref: torch.Tensor) -> float:
+    return float(torch.linalg.vector_norm(out - ref) / torch.linalg.vector_norm(ref).clamp_min(1e-30))
+
+
+def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, tp: int = 1, steps: int = 10,
+               warmup: int = 2, min_gain: float = 0.01, rounds: int = 2, rtol: float = 1e-4,
+               quiet: bool = False) -> list[TuneResult]:
+    """Tune each launch shape of a model's projection sweep inside the sweep.
+
+    For each token count, the sweep's launches (mambo_amd.utils.sweep) are replayed from
+    a HIP graph with one launch shape's configuration set to each of its candidates and
+    every other shape at its current choice (the tuned table's, then the winners of the
+    shapes tuned before it), and the step time is what decides: a launch between its
+    neighbours differs from one timed alone, whose clocks and caches no earlier launch
+    has touched. A candidate whose outputs differ from the library default's by more than
+    `rtol` (relative L2) counts as a failure. The winner, re-timed alternately with the
+    library default for `rounds` rounds, replaces it only if the step is at least
+    `min_gain` (a fraction of the step time) faster. tuner_us and default_us are step
+    times; mean_us, batched_us and event_us time one launch of the shape alone with the
+    reference's three timers."""
+    from mambo_amd.kernels.iq3_s_fp8 import default_config, gemm_search_space, select_config, tuned_key
+    from mambo_amd.utils.sweep import MODELS, build_launches, build_weights, capture, launch_shape, make_step, \
+        time_replays
+
+    layers = MODELS[model][1] if layers is None else layers
+    weights = build_weights(model, layers, tp)
+    stream = torch.cuda.current_stream()
+    results = []
+    for m in tokens:
+        launches = build_launches(weights, m)
+        shapes = [launch_shape(projs) for _, projs, _ in launches]
+        keys = list(dict.fromkeys(shapes))
+        chosen = {key: select_config(m, *key) for key in keys}
+        default = default_config(m)
+        make_step(launches, [default] * len(launches))()
+        torch.cuda.synchronize()
+        outputs = {key: list({id(p[3]): p[3] for (_, projs, _), s in zip(launches, shapes) if s == key
+                              for p in projs}.values()) for key in keys}
+        refs = {key: [o.clone() for o in outs] for key, outs in outputs.items()}
+
+        def step_us(key, config) -> float:
+            configs = [config if s == key else chosen[s] for s in shapes]
+            step = make_step(launches, configs)
+            step()  # eager first: an invalid configuration raises here, before capture
+            torch.cuda.synchronize()
+            for out, ref in zip(outputs[key], refs[key]):
+                err = _rel_l2(out, ref)
+                if not err <= rtol:
+                    raise RuntimeError(f"output differs from the library default's (rel-L2 {err:.3g})")
+            graph = capture(step)
+            ms, _ = time_replays(graph.replay, steps, warmup)
+            del graph
+            return ms * 1e3
+
+        for key in keys:
+            successes, failures = [], []
+            for config in gemm_search_space(m, *key):
+                try:
+                    successes.append((config, step_us(key, config)))
+                except (ValueError, RuntimeError) as exc:
+                    failures.append((config, str(exc)))
+            if not successes:
+                raise RuntimeError(f"M={m} {key}: no configuration ran ({failures[:3]})")
+            best, tuner_us = min(successes, key=lambda item: item[1])
+            default_us = next((us for config, us in successes if config == default), None)
+            if default_us is not None:
+                if best != default:
+                    default_us = tuner_us = float("inf")
+                    for _ in range(rounds):
+                        default_us = min(default_us, step_us(key, default))
+                        tuner_us = min(tuner_us, step_us(key, best))
+                if tuner_us > default_us * (1.0 - min_gain):
+                    best, tuner_us = default, default_us
+            chosen[key] = best
+            one = make_step([launches[shapes.index(key)]], [best])
+            mean_us = _host_time(stream, one, drain_each=True)
+            batched_us = _host_time(stream, one, drain_each=False)
+            event_us = _time_events(stream, one, 20)
+            result = TuneResult(f"M={m} N={key[0]} K={key[1]} in the {model} sweep", tuned_key(*key, m), dict(best),
+                                mean_us, batched_us, event_us, tuner_us, successes, failures, default_us,
+                                dict(default))
+            results.append(result)
+            if not quiet:
+                versus = "" if default_us is None else (
+                    " (library default)" if result.is_default else f" (library default {default_us:.1f})")
+                print(f"{result.case}: best_config={best}, step_us={tuner_us:.1f}{versus}, one launch alone: "
+                      f"mean_us={mean_us:.3f}, batched_us={batched_us:.3f}, event_us={event_us:.3f}, "
+                      f"candidates={len(successes)} passed/{len(failures)} failed", flush=True)
+        del launches, outputs, refs
+        torch.cuda.empty_cache()
+    return results
+
+
 def load_gguf_weight(model: Path, weight_name: str, expected_type: str) -> torch.Tensor:
     """The named 2-D block-quantized GGUF tensor as u8 [N, K/block_elements, block_bytes]
     on the current GPU (the reference's load_gguf_weight, kernel_benchmark.py:103-122;
@@ -247,17 +344,36 @@ def benchmark_main(argv: Sequence[str] | None = None) -> list[TuneResult]:
     parser.add_argument("--weight-name", help="tensor name in the GGUF model")
     parser.add_argument("--synthetic", nargs=2, type=int, metavar=("N", "K"), action="append",
                         help="use a random IQ3_S weight of this shape instead of a GGUF tensor (repeatable)")
+    parser.add_argument("--sweep", choices=["llama70b", "llama8b"],
+                        help="tune every launch shape of this model's projection sweep inside the replayed sweep "
+                             "(iq3_s_fp8 only) instead of one weight at a time")
+    parser.add_argument("--layers", type=int, help="layers of the --sweep (default: all of the model's)")
+    parser.add_argument("--tp", type=int, default=1, help="--sweep one GPU's shard at this tensor parallelism")
+    parser.add_argument("--steps", type=int, default=10, help="timed sweep replays per --sweep candidate")
     parser.add_argument("--tokens", type=int, nargs="+", default=[4, 128], help="token counts M to tune")
     parser.add_argument("--write-table", action="store_true", help="store winners in the tuned table")
     parser.add_argument("--table", type=Path, help="tuned table to write (default: the one the launcher reads)")
     parser.add_argument("--rotate-mib", type=int, default=512,
                         help="weight copies per case to at least this many MiB (at most 64 copies)")
-    parser.add_argument("--min-gain", type=float, default=0.03,
-                        help="fraction by which a candidate must beat the library default")
+    parser.add_argument("--min-gain", type=float, default=None,
+                        help="fraction by which a candidate must beat the library default (default 0.03 of the "
+                             "launch time; with --sweep 0.01 of the step time)")
     parser.add_argument("--no-graph", action="store_true", help="time candidates by eager launches")
     args = parser.parse_args(argv)
 
     expected_type, kernel_module, factory = _BENCHMARKS[args.kernel]
+    if args.sweep:
+        if args.kernel != "iq3_s_fp8" or args.no_graph or args.synthetic or args.model:
+            parser.error("--sweep tunes iq3_s_fp8 from replayed graphs of its own synthetic weights")
+        module = importlib.import_module(kernel_module)
+        results = sweep_tune(args.sweep, args.tokens, layers=args.layers, tp=args.tp, steps=args.steps,
+                             min_gain=0.01 if args.min_gain is None else args.min_gain)
+        if args.write_table:
+            from mambo_amd import _native
+            write_tuned_table(results, args.table or module.TUNED_PATH, _native.device_arch())
+        return results
+    if args.min_gain is None:
+        args.min_gain = 0.03
     if args.synthetic:
         sources = [lambda shape=shape: synthetic_weight(*shape) for shape in args.synthetic]
     elif args.model and args.weight_name:

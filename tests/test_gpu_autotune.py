@@ -128,3 +128,39 @@ def test_benchmark_command_on_a_gguf_file(gpu, tmp_path, capsys):
         assert key in (iq3_s_fp8.tuned_key(n, k, 4), iq3_s_fp8.tuned_key(n, k, 32)), key
         c = _native.GemmConfig.from_dict(cfg)
         assert _native.lib().mambo_gemm_check_config(int(key.split("@")[1]), n, k // 256, ctypes.byref(c)) == 0
+
+
+@pytest.mark.timeout(300)
+def test_sweep_tuner_on_one_layer(gpu, tmp_path, capsys):
+    """`--sweep llama8b --layers 1`: every candidate of each of the layer's four launch
+    shapes runs inside the replayed layer and matches the library default's outputs (a
+    mismatch would be a failure), and the table gets an entry exactly for the shapes whose
+    winner beat the default."""
+    import ctypes
+    import json
+
+    from mambo_amd import _native
+    from mambo_amd.kernels import iq3_s_fp8
+    from mambo_amd.utils.kernel_benchmark import benchmark_main
+    shapes = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]  # q/k/v, o, gate/up, down
+    table = tmp_path / "tuned.json"
+    step("benchmark_main iq3_s_fp8 --sweep llama8b --layers 1 --tokens 1 16 --steps 3 --write-table")
+    results = benchmark_main(["iq3_s_fp8", "--sweep", "llama8b", "--layers", "1", "--tokens", "1", "16",
+                              "--steps", "3", "--write-table", "--table", str(table)])
+    text = capsys.readouterr().out
+    assert [r.key for r in results] == [iq3_s_fp8.tuned_key(n, k, m) for m in (1, 16) for n, k in shapes]
+    written = json.loads(table.read_text())["gfx950"]
+    for r, (m, (n, k)) in zip(results, [(m, s) for m in (1, 16) for s in shapes]):
+        assert f"{r.case}: best_config=" in text
+        assert not r.failures, r.failures[:3]
+        assert len(r.successes) == len(iq3_s_fp8.gemm_search_space(m, n, k))
+        assert r.best in iq3_s_fp8.gemm_search_space(m, n, k)
+        assert r.default_of == iq3_s_fp8.default_config(m) and r.default_us is not None
+        assert r.mean_us > 0 and r.batched_us > 0 and r.event_us > 0 and r.tuner_us > 0
+        assert r.is_default or r.tuner_us <= 0.99 * r.default_us
+        if r.is_default:
+            assert r.key not in written
+        else:
+            assert written[r.key] == r.best
+            c = _native.GemmConfig.from_dict(r.best)
+            assert _native.lib().mambo_gemm_check_config(m, n, k // 256, ctypes.byref(c)) == 0
