@@ -468,8 +468,12 @@ __device__ __forceinline__ void stream_tile_end(float (&acc)[U][4], float *red, 
 // itself (quantize_group32: the quantizer's arithmetic, so the codes are identical), in
 // place of a separate quantizer launch; xs is unused.
 // kLg: log2 of the codebook copies in LDS (see RepGrid).
+// At most 256 registers per lane (two waves per SIMD): the compiler then keeps the MFMA
+// results in VGPRs. Allowed the full 512 of one wave per SIMD (4-wave workgroups), it
+// wrote them to AGPRs and read each back (8 v_accvgpr_read per block) and needed 84
+// registers instead of 71 at one token: 70B M=1 sweep +0.5%, M=2 +1.2%, 8B M=1 +0.7%.
 template <int U, int W, bool kLdsAct, int kQ = 0, int kLg = 0>
-__global__ __launch_bounds__(W * 64) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_stream_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                              const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                              GroupArgs ga, int64_t ntiles, int tpw, int B, int bps,
                                                              int atomic)
