@@ -395,9 +395,10 @@ def roofline_of(r: dict, mfma_bound: bool, workload: str) -> dict:
 
 
 # Further points of the M = 1..8192 metric timed by the default run, after the headline:
-# the Llama-3-70B sweep at 16 tokens (same weights) and the Llama-3-8B sweep at the two
-# prefill sizes (32 layers, 3.0 GB of weights built after the 70B ones are freed).
-DEFAULT_POINTS = "llama70b:16,llama8b:2048,llama8b:8192"
+# the Llama-3-70B sweep at 16, 32 and 512 tokens (same weights), then the Llama-3-8B
+# sweep at the decode sizes 1, 4 and 16 and the prefill sizes 2048 and 8192 (32 layers,
+# 3.0 GB of weights built after the 70B ones are freed).
+DEFAULT_POINTS = "llama70b:16,llama70b:32,llama70b:512,llama8b:1,llama8b:4,llama8b:16,llama8b:2048,llama8b:8192"
 
 
 def sweep_points(args, held: list) -> list:
