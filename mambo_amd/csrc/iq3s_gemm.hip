@@ -88,6 +88,8 @@ __host__ __device__ constexpr int stream_lut_bytes(int lg) { return 2048 << lg; 
 #endif
 constexpr int kDepth = MAMBO_STREAM_DEPTH;
 
+// Scheduler fences that keep each step's prefetch loads ahead of its decode (without
+// them the compiler sinks the loads toward their use and the ring stops overlapping).
 #ifndef MAMBO_SCHED_FENCE
 #define MAMBO_SCHED_FENCE 1
 #endif
