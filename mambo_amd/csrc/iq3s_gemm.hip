@@ -1984,6 +1984,16 @@ mambo_gemm_config family_default(int kernel, int64_t m, int64_t n, int64_t block
             // 4-10% ahead of 128 x 128 x 8)
             wgs = w128;
             c.tile_m = 256;
+        } else if (fits256 && long_k && w128 < kCUs && cdiv(kCUs, w128) <= blocks / 16 &&
+                   rounds_full(w128 * cdiv(kCUs, w128))) {
+            // long K with too few 256 x 128 items for a round: the prefill form with a K
+            // split that fills one round (at least 16 blocks per split). Against the
+            // 128-token tile's wider split, whole sweeps: 70B M=256 +1.2-1.5%, 8B M=1024
+            // +0.4-0.9%; where the split cannot fill a round (8B down at 512 and 768
+            // tokens: capped at 3 splits, or 1.125 rounds) it lost 1-5%, so it stays off
+            wgs = w128;
+            c.tile_m = 256;
+            c.split_k = (int32_t)cdiv(kCUs, w128);
         } else if (fits128 && ((wgs = cdiv(rt, 8) * cdiv(m, 128)) >= kCUs || long_k)) {
             c.tile_m = 128;
             if (long_k && wgs < 2 * kCUs)
