@@ -126,8 +126,10 @@ def test_gemm_config_defaults_and_validation():
     # per CU) fills at least 7/8 of the CUs (and the tokens are padded by at most 1/8 more
     # than with 128-token tiles), else 256 x 128 x 8 under the same rule, else
     # 128 x 128 x 8 when that gives every CU a workgroup (padding at most 1/8 over 64-token
-    # tiles), else 64 x 128 x 8; on long K (>= 48 blocks) the 128-token tile with K split
-    # until the grid covers the chip twice
+    # tiles), else 64 x 128 x 8; 256 x 128 x 8 also where both 256-token grids fill their
+    # rounds and its rounds are at least 8% fuller; on long K (>= 48 blocks) 256 x 128 x 8
+    # with a K split that fills one round when there is one (at least 16 blocks per
+    # split), else the 128-token tile with K split until the grid covers the chip twice
     for m, n, blocks, tile, split in ((2048, 4096, 32, (256, 128, 8), 1), (2048, 4096, 16, (256, 128, 8), 1),
                                       (2048, 4096, 56, (256, 128, 8), 1), (8192, 4096, 16, (256, 256, 16), 1),
                                       (8192, 14336, 32, (256, 256, 16), 1),
@@ -136,9 +138,12 @@ def test_gemm_config_defaults_and_validation():
                                       (2048, 10240, 32, (128, 128, 8), 1), (8192, 10240, 32, (256, 256, 16), 1),
                                       (256, 8192, 32, (64, 128, 8), 1), (64, 57344, 32, (64, 128, 8), 1),
                                       (128, 57344, 32, (128, 128, 8), 1), (384, 57344, 32, (128, 128, 8), 1),
-                                      (192, 57344, 32, (64, 128, 8), 1), (256, 8192, 112, (128, 128, 8), 4),
-                                      (512, 8192, 112, (128, 128, 8), 2), (2048, 8192, 112, (256, 256, 16), 1),
-                                      (512, 4096, 56, (128, 128, 8), 3), (128, 8192, 112, (128, 128, 8), 7)):
+                                      (192, 57344, 32, (64, 128, 8), 1), (256, 8192, 112, (256, 128, 8), 4),
+                                      (512, 8192, 112, (256, 128, 8), 2), (2048, 8192, 112, (256, 256, 16), 1),
+                                      (512, 4096, 56, (128, 128, 8), 3), (768, 4096, 56, (128, 128, 8), 3),
+                                      (1024, 4096, 56, (256, 128, 8), 2), (768, 8192, 112, (128, 128, 8), 2),
+                                      (2048, 28672, 16, (256, 128, 8), 1), (1536, 28672, 16, (256, 256, 16), 1),
+                                      (1024, 57344, 32, (256, 128, 8), 1), (128, 8192, 112, (128, 128, 8), 7)):
         c = _native.GemmConfig()
         assert lib.mambo_gemm_default_config(m, n, blocks, ctypes.byref(c)) == 0
         assert (c.kernel, c.tile_m, c.tile_n, c.waves, c.split_k) == (_native.GEMM_TILED, *tile, split), \
