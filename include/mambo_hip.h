@@ -11,6 +11,10 @@
  *     crosses this boundary. The Python layer maps ERR_VALUE -> ValueError,
  *     ERR_TYPE -> TypeError, everything else -> RuntimeError, as the reference
  *     launchers raise them.
+ *   - A call that launches kernels first takes the thread's pending HIP error
+ *     (hipGetLastError), so the failures it reports are its own; an error left pending
+ *     by earlier, unrelated HIP work is then gone from hipGetLastError, and the call,
+ *     if it succeeds, names it in mambo_last_error().
  *
  * Each entry point names the reference interface it replaces (paths are in the
  * Menooker/Mambo reference). The reference launches cuTile kernels with

@@ -16,11 +16,25 @@ int mambo_fail(int status, const char *fmt, ...)
     return status;
 }
 
+// An error found on the thread before one of this call's launches (hipSuccess: none).
+static thread_local hipError_t g_prior_error = hipSuccess;
+
+void mambo_note_prior_error(hipError_t err)
+{
+    if (err != hipSuccess && g_prior_error == hipSuccess)
+        g_prior_error = err;
+}
+
 int mambo_check_launch(const char *what)
 {
+    const hipError_t prior = g_prior_error;
+    g_prior_error = hipSuccess;
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
         return mambo_fail(MAMBO_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(err));
+    if (prior != hipSuccess) // the call succeeded; keep the earlier error readable
+        return mambo_fail(MAMBO_OK, "%s: ok; an earlier HIP error left on this thread was taken off it before "
+                                    "the launch: %s", what, hipGetErrorString(prior));
     g_last_error[0] = '\0';
     return MAMBO_OK;
 }

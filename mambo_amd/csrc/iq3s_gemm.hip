@@ -1650,9 +1650,10 @@ __global__ __launch_bounds__(W * 64) void gemm_prefill_kernel(const uint8_t *__r
 // Zero rows [0, M) of projection blockIdx.y's output (the split-K accumulators of every
 // projection of a launch in one dispatch): each thread clears a 4-float chunk of a row
 // (chunks flattened over rows, grid-strided), with one 16-byte store where the chunk is
-// whole and 16-byte aligned (column slices of a wider buffer may not be). The host keeps
-// M times the chunks per row below 2^31. The projection is picked by selects over
-// constant indices, so the arguments stay in scalar registers.
+// whole and 16-byte aligned (column slices of a wider buffer may not be). The chunk index
+// is 64-bit: the grid stride (up to 1024 x 256) added to an index near the end of a large
+// output must not wrap. The projection is picked by selects over constant indices, so the
+// arguments stay in scalar registers.
 __global__ __launch_bounds__(256) void zero_rows_kernel(GroupArgs ga, int M)
 {
     const int g = blockIdx.y;
@@ -1665,15 +1666,15 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(GroupArgs ga, int M)
             cols = ga.n[i];
             ld = ga.ldo[i];
         }
-    const int chunks = (int)((cols + 3) / 4);
-    const int total = M * chunks;
-    for (int i = (int)blockIdx.x * 256 + (int)threadIdx.x; i < total; i += (int)gridDim.x * 256) {
-        const int r = i / chunks, c = 4 * (i - r * chunks);
+    const int64_t chunks = (cols + 3) / 4;
+    const int64_t total = (int64_t)M * chunks;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / chunks, c = 4 * (i - r * chunks);
         float *p = out + r * ld + c;
         if (c + 4 <= cols && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
             __builtin_nontemporal_store(v4f{0.0f, 0.0f, 0.0f, 0.0f}, reinterpret_cast<v4f *>(p));
         } else {
-            for (int j = c; j < cols && j < c + 4; ++j)
+            for (int64_t j = c; j < cols && j < c + 4; ++j)
                 __builtin_nontemporal_store(0.0f, out + r * ld + j);
         }
     }

@@ -7,16 +7,21 @@
 #include "iq3s_grid.h"
 
 // ----------------------------------------------------------------------------- errors
-// Thread-local last error (api.cpp). Entry points return a MAMBO_* status.
+// Thread-local last error (api.hip). Entry points return a MAMBO_* status.
 int mambo_fail(int status, const char *fmt, ...);
 int mambo_check_launch(const char *what);
+// Records an error that earlier, unrelated HIP work left on the calling thread (taken
+// off the thread by the hipGetLastError in MAMBO_LAUNCH); mambo_check_launch then
+// reports it through mambo_last_error() (the call itself still succeeds).
+void mambo_note_prior_error(hipError_t err);
 
-// Launch with the calling thread's HIP error state cleared first, so that the
+// Launch with the calling thread's HIP error state taken first, so that the
 // mambo_check_launch after it reports this launch's own failure, not one that an
-// earlier, unrelated HIP call left behind.
+// earlier, unrelated HIP call left behind; that earlier error stays readable through
+// mambo_last_error().
 #define MAMBO_LAUNCH(...)                                                                          \
     do {                                                                                           \
-        (void)hipGetLastError();                                                                   \
+        mambo_note_prior_error(hipGetLastError());                                                 \
         hipLaunchKernelGGL(__VA_ARGS__);                                                           \
     } while (0)
 

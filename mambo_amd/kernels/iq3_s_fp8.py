@@ -35,7 +35,9 @@ from mambo_amd.utils.iq3_s_weight import (
     _weight_dimensions,
     _weight_kernel_args,
     ensure_packed,
+    has_soa_fields,
     prepare_iq3_s_fields,
+    release_soa_fields,
 )
 
 IQ3_S_SCALE_VALUES = 32
@@ -97,11 +99,12 @@ def iq3_s_fp8_table() -> np.ndarray:
 
 
 def _get_iq3_table() -> torch.Tensor:
-    """FP8-encoded codebook on the current device (iq3_s_fp8.py:97-102). The kernels
-    carry their own copy in the code object; this tensor is for callers that want it."""
+    """FP8-encoded codebook, uint32 [512], uploaded once per device and cached
+    (iq3_s_fp8.py:97-102). The kernels carry their own copy in the code object; this
+    tensor is for callers that want it."""
     device = torch.cuda.current_device()
     if device not in _IQ3_TABLES:
-        _IQ3_TABLES[device] = torch.from_numpy(iq3_s_fp8_table().view(np.int32)).to(f"cuda:{device}")
+        _IQ3_TABLES[device] = torch.from_numpy(iq3_s_fp8_table().copy()).to(f"cuda:{device}")
     return _IQ3_TABLES[device]
 
 
@@ -118,6 +121,9 @@ def launch_dequant_iq3_s(iq3_weight: IQ3SFields, *, tile_n: int = 1, stream=None
     """
     _power_of_two(tile_n, "tile_n")
     n_rows, blocks = _weight_dimensions(iq3_weight)
+    if not has_soa_fields(iq3_weight):
+        raise ValueError("the decoder reads the SoA fields; this weight holds only its tile layout "
+                         "(prepared with fields=False, or after release_soa_fields)")
     fields = _weight_kernel_args(iq3_weight)
     for name, t in zip(("d", "qs", "qh", "signs", "scales"), fields):
         if not t.is_contiguous() or t.numel() == 0 and n_rows * blocks:

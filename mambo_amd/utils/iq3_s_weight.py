@@ -30,10 +30,10 @@ class IQ3SFields:
     launch_iq3_s_fp8_matmul builds it from the fields on first use).
 
     The packed tile is a cache of the SoA fields. It remembers which field tensors
-    (storage and in-place version) it was built from, and the launchers rebuild it when
+    (address and in-place version) it was built from, and the launchers rebuild it when
     a field has been written in place or replaced (``dataclasses.replace``) since. A
-    weight prepared with ``fields=False`` has placeholder fields; its packed tile is the
-    weight itself.
+    weight prepared with ``fields=False``, or whose fields were given up with
+    ``release_soa_fields``, has placeholder fields; its packed tile is the weight itself.
     """
 
     d: torch.Tensor
@@ -51,10 +51,12 @@ PACKED_ONLY = ("packed-only",)
 
 
 def fields_signature(fields: IQ3SFields) -> tuple:
-    """Identity of the SoA field tensors: storage address, view offset and in-place
-    version counter of each (a write through any view of a tensor bumps its counter)."""
-    return tuple((t.untyped_storage().data_ptr(), t.storage_offset(), t._version)
-                 for t in _weight_kernel_args(fields))
+    """Identity of the SoA field tensors: data address (storage plus view offset) and
+    in-place version counter of each (a write through any view of a tensor bumps its
+    counter; ``set_`` bumps it too, and assigning ``.data`` moves the address). About
+    half the host time of asking each tensor for its storage and offset, on every
+    launch of a weight that keeps its fields."""
+    return tuple((t.data_ptr(), t._version) for t in _weight_kernel_args(fields))
 
 
 def _check_raw(iq3_weight) -> tuple[int, int]:
@@ -74,19 +76,24 @@ def packed_bytes(n: int, blocks: int) -> int:
     return int(_native.lib().mambo_iq3s_packed_bytes(n, blocks))
 
 
-def prepare_iq3_s_fields(iq3_weight: torch.Tensor, *, fields: bool = True, stream=None) -> IQ3SFields:
+def prepare_iq3_s_fields(iq3_weight: torch.Tensor, *, fields: bool = True, pack: bool = False,
+                         stream=None) -> IQ3SFields:
     """Split GGUF uint8 [N,B,110] blocks into SoA fields (and the tile layout) once.
 
     Follows prepare_iq3_s_fields (iq3_s_weight.py:25-54): any strides and any byte
-    alignment of the source are accepted; every bit is preserved. ``fields=False``
-    builds only the tile layout (the SoA tensors are then empty placeholders), which
-    halves the memory of very large weights that are only multiplied.
+    alignment of the source are accepted; every bit is preserved. By default only the
+    SoA fields are built, as in the reference (110 bytes per block); the tile layout the
+    projection kernels read (another 110 bytes per block) is built from them on the
+    first launch and cached. ``pack=True`` builds both now, in one pass over the source.
+    ``fields=False`` builds only the tile layout (the SoA tensors are then empty
+    placeholders), which halves the memory of very large weights that are only
+    multiplied; ``release_soa_fields`` does the same for a weight prepared with fields.
     """
     n, blocks = _check_raw(iq3_weight)
     dev = iq3_weight.device
     L = _native.lib()
     with torch.cuda.device(dev):
-        packed = torch.empty(packed_bytes(n, blocks), dtype=torch.uint8, device=dev)
+        packed = torch.empty(packed_bytes(n, blocks), dtype=torch.uint8, device=dev) if pack or not fields else None
         if fields:
             d = torch.empty((blocks, n), dtype=torch.float16, device=dev)
             qs = torch.empty((blocks, n, 16), dtype=torch.uint32, device=dev)
@@ -96,21 +103,50 @@ def prepare_iq3_s_fields(iq3_weight: torch.Tensor, *, fields: bool = True, strea
             ptrs = [d.data_ptr(), qs.data_ptr(), qh.data_ptr(), signs.data_ptr(), scales.data_ptr()]
         else:
             # zero-stride placeholders: right shapes, no memory
-            def ph(dtype, *shape):
-                return torch.zeros((), dtype=dtype, device=dev).expand(*shape)
-            d = ph(torch.float16, blocks, n)
-            qs = ph(torch.uint32, blocks, n, 16)
-            qh = ph(torch.uint16, blocks, n, 4)
-            signs = ph(torch.int32, blocks, n, 8)
-            scales = ph(torch.uint32, blocks, n)
+            d = _placeholder(torch.float16, (blocks, n), dev)
+            qs = _placeholder(torch.uint32, (blocks, n, 16), dev)
+            qh = _placeholder(torch.uint16, (blocks, n, 4), dev)
+            signs = _placeholder(torch.int32, (blocks, n, 8), dev)
+            scales = _placeholder(torch.uint32, (blocks, n), dev)
             ptrs = [None] * 5
         sn, sb, sbyte = iq3_weight.stride()
         _native.check(L.mambo_iq3s_prepare(iq3_weight.data_ptr(), n, blocks, sn, sb, sbyte, *ptrs,
-                                           packed.data_ptr(), _native.stream_handle(stream)),
+                                           None if packed is None else packed.data_ptr(),
+                                           _native.stream_handle(stream)),
                       "prepare_iq3_s_fields")
     result = IQ3SFields(d, qs, qh, signs, scales, packed)
-    object.__setattr__(result, "packed_from", fields_signature(result) if fields else PACKED_ONLY)
+    if packed is not None:
+        object.__setattr__(result, "packed_from", fields_signature(result) if fields else PACKED_ONLY)
     return result
+
+
+def _placeholder(dtype, shape, dev) -> torch.Tensor:
+    """A zero-stride tensor of the field's dtype and shape that takes no memory."""
+    return torch.zeros((), dtype=dtype, device=dev).expand(*shape)
+
+
+def release_soa_fields(iq3_weight: IQ3SFields, stream=None) -> IQ3SFields:
+    """Keep only the tile layout of a prepared weight: the packed tile is built (if it is
+    not current), then the five SoA fields are replaced in place by zero-stride
+    placeholders of the same shapes and dtypes, so their memory (110 bytes per block)
+    is freed once nothing else holds them. Projections keep working and return the same
+    results; reading the fields, or ``launch_dequant_iq3_s``, no longer gives the
+    weight (the latter raises ValueError). For callers that only multiply: those that
+    read the fields keep them by not calling this. Returns the same object."""
+    ensure_packed(iq3_weight, stream)
+    if iq3_weight.packed_from != PACKED_ONLY:
+        dev = iq3_weight.d.device
+        for name in ("d", "qs", "qh", "signs", "scales"):
+            t = getattr(iq3_weight, name)
+            object.__setattr__(iq3_weight, name, _placeholder(t.dtype, t.shape, dev))
+        object.__setattr__(iq3_weight, "packed_from", PACKED_ONLY)
+    return iq3_weight
+
+
+def has_soa_fields(iq3_weight: IQ3SFields) -> bool:
+    """Whether the SoA fields hold the weight (False after fields=False or
+    release_soa_fields)."""
+    return iq3_weight.packed_from != PACKED_ONLY
 
 
 def _weight_dimensions(iq3_weight: IQ3SFields) -> tuple[int, int]:

@@ -234,7 +234,7 @@ def _rel_l2(out: torch.Tensor, ref: torch.Tensor) -> float:
 
 def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, tp: int = 1, steps: int = 10,
                warmup: int = 2, min_gain: float = 0.01, rounds: int = 2, rtol: float = 1e-4,
-               quiet: bool = False) -> list[TuneResult]:
+               quiet: bool = False, progress: int = 10) -> list[TuneResult]:
     """Tune each launch shape of a model's projection sweep inside the sweep.
 
     For each token count, the sweep's launches (mambo_amd.utils.sweep) are replayed from
@@ -247,7 +247,8 @@ def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, 
     library default for `rounds` rounds, replaces it only if the step is at least
     `min_gain` (a fraction of the step time) faster. tuner_us and default_us are step
     times; mean_us, batched_us and event_us time one launch of the shape alone with the
-    reference's three timers."""
+    reference's three timers. Unless quiet, a progress line (candidates done, failures,
+    the best so far) is printed every `progress` candidates of a shape (0: none)."""
     from mambo_amd.kernels.iq3_s_fp8 import default_config, gemm_search_space, select_config, tuned_key
     from mambo_amd.utils.sweep import MODELS, build_launches, build_weights, capture, launch_shape, make_step, \
         time_replays
@@ -289,11 +290,19 @@ def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, 
 
         for key in keys:
             successes, failures = [], []
-            for config in gemm_search_space(m, *key):
+            space = gemm_search_space(m, *key)
+            for i, config in enumerate(space):
                 try:
                     successes.append((config, step_us(key, config)))
                 except (ValueError, RuntimeError) as exc:
                     failures.append((config, str(exc)))
+                # one line per `progress` candidates (each is an eager step, a capture and
+                # the replays), so a long search over a large sweep keeps reporting
+                if not quiet and progress and ((i + 1) % progress == 0 or i + 1 == len(space)):
+                    lead = min(successes, key=lambda item: item[1]) if successes else None
+                    best_text = f"best so far {lead[0]} at {lead[1]:.1f} us" if lead else "none ran yet"
+                    print(f"[tune] M={m} N={key[0]} K={key[1]}: candidate {i + 1}/{len(space)}, "
+                          f"{len(failures)} failed, {best_text}", flush=True)
             if not successes:
                 raise RuntimeError(f"M={m} {key}: no configuration ran ({failures[:3]})")
             best, tuner_us = min(successes, key=lambda item: item[1])

@@ -123,6 +123,37 @@ def test_packed_cache_follows_the_soa_fields():
     assert packed_is_current(p)
 
 
+
+def test_release_soa_fields_keeps_only_the_tile():
+    """release_soa_fields: with a current packed tile, the five SoA fields become
+    zero-stride placeholders of the same shapes and dtypes (their tensors are freed once
+    nothing else holds them), the tile is kept and stays current, and the standalone
+    decoder, which reads the fields, refuses the weight."""
+    import gc
+    import weakref
+
+    from mambo_amd.kernels.iq3_s_fp8 import launch_dequant_iq3_s
+    from mambo_amd.utils.iq3_s_weight import (IQ3SFields, fields_signature, has_soa_fields, packed_is_current,
+                                              release_soa_fields)
+    blocks, n = 3, 32
+    f = IQ3SFields(torch.ones(blocks, n, dtype=torch.float16), torch.ones(blocks, n, 16, dtype=torch.uint32),
+                   torch.ones(blocks, n, 4, dtype=torch.uint16), torch.ones(blocks, n, 8, dtype=torch.int32),
+                   torch.ones(blocks, n, dtype=torch.uint32), torch.zeros(blocks * n * 110, dtype=torch.uint8))
+    object.__setattr__(f, "packed_from", fields_signature(f))
+    shapes = [(t.shape, t.dtype) for t in (f.d, f.qs, f.qh, f.signs, f.scales)]
+    refs = [weakref.ref(t) for t in (f.d, f.qs, f.qh, f.signs, f.scales)]
+    tile = f.packed
+    assert has_soa_fields(f) and packed_is_current(f)
+    assert release_soa_fields(f) is f
+    gc.collect()
+    assert all(r() is None for r in refs)  # the SoA tensors are gone
+    assert f.packed is tile and packed_is_current(f) and not has_soa_fields(f)
+    for t, (shape, dtype) in zip((f.d, f.qs, f.qh, f.signs, f.scales), shapes):
+        assert t.shape == shape and t.dtype == dtype and all(st == 0 for st in t.stride())
+    assert release_soa_fields(f) is f and f.packed is tile  # a second release changes nothing
+    with pytest.raises(ValueError, match="SoA fields"):
+        launch_dequant_iq3_s(f)
+
 def test_activation_rows_are_copied_only_when_misaligned():
     from mambo_amd.kernels.iq3_s_fp8 import _aligned_rows
     base = torch.arange(4 * 96, dtype=torch.uint8).reshape(4, 96)

@@ -152,6 +152,11 @@ def test_sweep_tuner_on_one_layer(gpu, tmp_path, capsys):
     written = json.loads(table.read_text())["gfx950"]
     for r, (m, (n, k)) in zip(results, [(m, s) for m in (1, 16) for s in shapes]):
         assert f"{r.case}: best_config=" in text
+        # progress while searching: a line every 10 candidates and one after the last
+        total = len(iq3_s_fp8.gemm_search_space(m, n, k))
+        assert f"[tune] M={m} N={n} K={k}: candidate {total}/{total}, 0 failed, best so far" in text
+        if total >= 10:
+            assert f"[tune] M={m} N={n} K={k}: candidate 10/{total}," in text
         assert not r.failures, r.failures[:3]
         assert len(r.successes) == len(iq3_s_fp8.gemm_search_space(m, n, k))
         assert r.best in iq3_s_fp8.gemm_search_space(m, n, k)

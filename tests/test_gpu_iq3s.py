@@ -22,7 +22,7 @@ def test_soa_fields_preserve_every_byte(gpu, n_rows, blocks):
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
     raw = make_synthetic_iq3_s(n_rows, blocks * 256, seed=0x50A)
     step(f"prepare [{n_rows},{blocks},110]")
-    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu), pack=True)
     torch.cuda.synchronize()
     reconstructed = np.empty_like(raw)
     for field, start, end in ((fields.d, 0, 2), (fields.qs, 2, 66), (fields.qh, 66, 74),
@@ -116,7 +116,8 @@ def test_pack_from_fields_matches_prepare(gpu):
     from mambo_amd.utils.iq3_s_weight import IQ3SFields, ensure_packed, prepare_iq3_s_fields
     raw = make_synthetic_iq3_s(45, 5 * 256, seed=3)
     step("prepare + pack from SoA [45,5,110]")
-    f = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    f = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu), pack=True)
+    assert prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu)).packed is None  # built on first launch
     g = IQ3SFields(f.d, f.qs, f.qh, f.signs, f.scales)
     packed = ensure_packed(g)
     torch.cuda.synchronize()
@@ -132,3 +133,48 @@ def test_gpu_generator_matches_oracle_rows(gpu):
                                                  _native.stream_handle(None)))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(raw.cpu().numpy(), oracle.gen_iq3s(0, rows, blocks, row0=1000))
+
+
+def test_get_iq3_table_is_the_decoders_codebook(gpu):
+    """_get_iq3_table (iq3_s_fp8.py:97-102): the E4M3-encoded codebook as uint32 [512] on
+    the current device, uploaded once and cached, equal to iq3_s_fp8_table(); and the
+    standalone decoder emits exactly its bytes: weight 4c + j of every code c of the
+    all-codes blocks is byte j of table[index c] with the weight's sign on bit 7."""
+    from mambo_amd.kernels import iq3_s_fp8 as mod
+    from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
+    step("_get_iq3_table on the current device")
+    table = mod._get_iq3_table()
+    assert table.device == gpu and table.dtype == torch.uint32 and tuple(table.shape) == (512,)
+    assert mod._get_iq3_table() is table
+    host = table.cpu().numpy()
+    np.testing.assert_array_equal(host, mod.iq3_s_fp8_table())
+    raw, code, sign = all_codes_blocks()
+    step("dequant all codes against the device table")
+    bits, _ = mod.launch_dequant_iq3_s(prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu)))
+    torch.cuda.synchronize()
+    mags = host[code].view(np.uint8).reshape(*code.shape, 4)  # byte j of each code's word
+    signs = ((sign[..., None] >> np.arange(4, dtype=np.uint16)) & 1).astype(np.uint8) << 7
+    expected = (mags | signs).reshape(raw.shape[0], -1)
+    np.testing.assert_array_equal(bits.cpu().numpy(), expected)
+
+
+def test_large_weight_kernel_args_views(gpu):
+    """_large_weight_kernel_args (iq3_s_weight.py:65-77): zero-copy views qh -> uint32
+    [B,N,2] and signs -> int32 [B,N*8]; d, qs and scales unchanged; the viewed bytes are
+    the raw blocks' qh and sign bytes."""
+    from mambo_amd.utils.iq3_s_weight import _large_weight_kernel_args, _weight_kernel_args, prepare_iq3_s_fields
+    n_rows, blocks = 37, 3
+    raw = make_synthetic_iq3_s(n_rows, blocks * 256, seed=0x1A6)
+    step(f"prepare [{n_rows},{blocks},110] for the large-MMA views")
+    fields = prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu))
+    d, qs, qh, signs, scales = _large_weight_kernel_args(fields)
+    base = _weight_kernel_args(fields)
+    assert d is base[0] and qs is base[1] and scales is base[4]
+    assert qh.dtype == torch.uint32 and tuple(qh.shape) == (blocks, n_rows, 2)
+    assert signs.dtype == torch.int32 and tuple(signs.shape) == (blocks, n_rows * 8)
+    assert qh.data_ptr() == fields.qh.data_ptr() and signs.data_ptr() == fields.signs.data_ptr()
+    torch.cuda.synchronize()
+    qh_bytes = qh.cpu().view(torch.uint8).numpy().reshape(blocks, n_rows, 8)
+    np.testing.assert_array_equal(qh_bytes.transpose(1, 0, 2), raw[..., 66:74])
+    sign_bytes = signs.cpu().view(torch.uint8).numpy().reshape(blocks, n_rows, 32)
+    np.testing.assert_array_equal(sign_bytes.transpose(1, 0, 2), raw[..., 74:106])

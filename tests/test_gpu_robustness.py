@@ -30,9 +30,15 @@ def test_stale_hip_error_is_not_blamed_on_the_next_launch(gpu):
     assert hip.hipSetDevice(9999) != 0
     rc = _native.lib().mambo_fill_f32(buf.data_ptr(), buf.numel(), 2.5, _native.stream_handle(None))
     assert rc == _native.MAMBO_OK, _native.lib().mambo_last_error()
+    # the earlier error is no longer pending on the thread, but the call names it
+    message = _native.lib().mambo_last_error().decode()
+    assert "earlier HIP error" in message and "fill_f32: ok" in message, message
     torch.cuda.synchronize()
     assert bool((buf == 2.5).all())
     assert hip.hipGetLastError() == 0
+    step("a second fill with nothing pending leaves no message")
+    rc = _native.lib().mambo_fill_f32(buf.data_ptr(), buf.numel(), 1.5, _native.stream_handle(None))
+    assert rc == _native.MAMBO_OK and _native.lib().mambo_last_error() == b""
 
 
 def test_packed_weight_follows_field_writes(gpu):
@@ -67,6 +73,41 @@ def test_packed_weight_follows_field_writes(gpu):
     check(second.cpu().numpy(), expected)
     assert not np.array_equal(second.cpu().numpy()[:, [7, 30]], first.cpu().numpy()[:, [7, 30]])
 
+
+
+def test_release_soa_fields_on_the_gpu(gpu):
+    """A weight prepared the reference's way holds only its SoA fields until the first
+    projection builds the tile; release_soa_fields then frees the fields (device memory
+    drops by their 110 bytes per block) and the next projections return the same bits."""
+    from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
+    from mambo_amd.utils.iq3_s_weight import has_soa_fields, prepare_iq3_s_fields, release_soa_fields
+    n, k, m = 512, 4096, 3
+    raw = make_synthetic_iq3_s(n, k, seed=0x5E1)
+    source = torch.from_numpy(raw).to(gpu)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(gpu)
+    step(f"prepare [{n},{k // 256},110] with SoA fields only")
+    fields = prepare_iq3_s_fields(source)
+    torch.cuda.synchronize()
+    soa = torch.cuda.memory_allocated(gpu) - base
+    assert fields.packed is None and soa >= raw.nbytes
+    xv, xs = oracle.quantize_mxfp8(np.random.default_rng(5).standard_normal((m, k)).astype(np.float32))
+    xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
+    step("first projection builds the tile")
+    first = launch_iq3_s_fp8_matmul(xvg, xsg, fields)
+    torch.cuda.synchronize()
+    check(first.cpu().numpy(), oracle.iq3s_fp8_matmul(xv, xs, raw))
+    assert fields.packed is not None
+    before = torch.cuda.memory_allocated(gpu)
+    step("release the SoA fields")
+    release_soa_fields(fields)
+    torch.cuda.synchronize()
+    assert not has_soa_fields(fields)
+    assert before - torch.cuda.memory_allocated(gpu) >= raw.nbytes
+    step("projection after the release")
+    second = launch_iq3_s_fp8_matmul(xvg, xsg, fields)
+    torch.cuda.synchronize()
+    assert torch.equal(second, first)
 
 def test_row_strided_scales_through_the_tiled_kernel(gpu):
     """M = 24 (the tiled kernel's 32-token tile by default on wide grids, and as an
