@@ -72,10 +72,14 @@ def run_gemm(args, weights=None):
     log(f"{len(projections)} projections in {len(launches)} launches, {weight_bytes / 1e9:.2f} GB of IQ3_S "
         "weights resident")
 
-    step = make_step(launches, configs, args.with_quant)
+    step = make_step(launches, configs, args.with_quant, chain=args.chain, chain_waves=args.chain_waves,
+                     chain_tpw=args.chain_tpw)
     outputs = list({id(o): o for (_, _, _, o) in projections}.values())
     step()
     torch.cuda.synchronize()
+    if args.chain:
+        from mambo_amd.kernels.iq3_s_fp8 import chain_status
+        chain_status(step.sync)  # a dependency wait that timed out stops the run here
     replay = step
     if not args.no_graph:
         # Capture one step on a side stream, then check one replay against eager results.
@@ -96,6 +100,9 @@ def run_gemm(args, weights=None):
         log("captured the step in a HIP graph; replay matches eager")
 
     ms, wall = time_replays(replay, args.steps, args.warmup)
+    if args.chain:
+        from mambo_amd.kernels.iq3_s_fp8 import chain_status
+        chain_status(step.sync)  # raises if any dependency wait of the timed replays timed out
     gbs = step_bytes / (ms * 1e-3) / 1e9
     tflops = step_flops / (ms * 1e-3) / 1e12
     log(f"{ms:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}), {gbs:.1f} GB/s, {tflops:.2f} TFLOP/s")
@@ -373,6 +380,9 @@ def gemm_workload_name(args) -> str:
     if args.with_quant != "none":
         grouping += {"separate": ", a quantizer launch before each GEMM launch",
                      "fused": ", quantization inside the GEMM launch where it fits (M <= 4)"}[args.with_quant]
+    if getattr(args, "chain", 0):
+        grouping += (f", {args.chain} consecutive launches per persistent chained launch (each launch's "
+                     "activation reads wait for the one before it)")
     model = "llama3-70b" if args.workload == "llama70b" else "llama3-8b"
     shard = f" (one GPU's shard at tensor parallelism {args.tp})" if args.tp > 1 else ""
     return f"{model} projection sweep{shard}: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
@@ -455,6 +465,11 @@ def main(argv=None) -> int:
                         "quantized once before timing, as the reference times the matmul alone")
     p.add_argument("--no-group", action="store_true",
                    help="one launch per projection (default: q/k/v and gate/up share a launch)")
+    p.add_argument("--chain", type=int, default=0,
+                   help="1..4 tokens: run each run of this many consecutive launches (at most 16) as one "
+                        "persistent chained launch, each launch waiting for the one before it")
+    p.add_argument("--chain-waves", type=int, default=0, help="waves per workgroup of the chained launches")
+    p.add_argument("--chain-tpw", type=int, default=0, help="16-row tiles per workgroup of the chained launches")
     p.add_argument("--points", default="auto",
                    help="further workload:m points timed after the headline, comma-separated, or 'none' "
                         f"(auto: {DEFAULT_POINTS} when the headline is the default 70B M=1 sweep)")

@@ -41,7 +41,11 @@ enum {
     MAMBO_ERR_UNSUPPORTED = -4  /* device is not gfx950 */
 };
 
-enum { MAMBO_DTYPE_F32 = 0, MAMBO_DTYPE_BF16 = 1 };
+enum {
+    MAMBO_DTYPE_F32 = 0,
+    MAMBO_DTYPE_BF16 = 1,
+    MAMBO_DTYPE_MXFP8 = 2 /* E4M3 values plus E8M0 scales per 32 (mambo_chain_launch only) */
+};
 
 /* Kernel families of the projection. */
 enum {
@@ -173,6 +177,56 @@ int mambo_iq3s_matmul_quantize_grouped(const void *x, int x_dtype, int64_t ldx, 
                                        const mambo_projection *proj, int count, int64_t blocks,
                                        const mambo_gemm_config *cfg, uint8_t *xv, int64_t ldxv,
                                        uint8_t *xs, int64_t ldxs, mambo_stream_t stream);
+
+/* Chained projections for 1..4 tokens: up to MAMBO_MAX_CHAIN launches, each as
+ * mambo_iq3s_fp8_matmul_grouped (1..MAMBO_MAX_GROUP projections of one input), run in
+ * order in ONE launch of the block-diagonal streaming kernel. No reference counterpart:
+ * the reference runs one launch_iq3_s_fp8_matmul per weight (iq3_s_fp8.py:364-399); this
+ * is for callers that run many projections back to back at decode sizes, such as a
+ * layer's q/k/v, o, gate/up and down or several layers. The outputs equal those of the
+ * separate grouped launches on one stream with the stream kernel at cfg->waves (4, 8 or
+ * 16) and no K split, bit for bit. Order: launch i reads its activations only after every
+ * output of launches < i is stored (device counters in `sync`), so launch i may take as
+ * its activations f32 or bf16 outputs of an earlier launch (x_dtype F32/BF16: rows
+ * quantized to MXFP8 in the kernel with the quantizer's arithmetic) - the semantics of
+ * the same launches on one stream. The workgroups of launch i+1 start streaming their
+ * weights while launch i drains. Every dependency wait is bounded (cfg->timeout_us,
+ * default 2 s); a wait that times out is reported by mambo_chain_status, the outputs then
+ * being undefined.
+ * sync: MAMBO_CHAIN_SYNC_WORDS uint32 of device memory (16.5 KiB: counters spread over
+ * lines of their own), zero before the first call; every call that does not time out
+ * leaves them zero again (a timeout is kept until mambo_chain_status reads it, which then
+ * clears every word). Calls that overlap in time must use different sync words.
+ * Allocates nothing. Measured slower than the same launches one by one on the Llama-3
+ * sweeps at 1 token (70B 0.92x, 8B 0.86x): it is the ordered-dependency form, not the
+ * fast path. */
+#define MAMBO_MAX_CHAIN 16
+#define MAMBO_CHAIN_SYNC_WORDS 4224
+typedef struct mambo_chain_launch {
+    const void *x;       /* MXFP8 values u8[m, ldx] (x_dtype MAMBO_DTYPE_MXFP8), or f32/bf16 rows */
+    int32_t x_dtype;     /* MAMBO_DTYPE_MXFP8, MAMBO_DTYPE_F32 or MAMBO_DTYPE_BF16 */
+    int32_t count;       /* projections in proj */
+    int64_t ldx;         /* row stride of x in elements; MXFP8: 16-byte multiple, else rows 16-byte aligned */
+    const uint8_t *xs;   /* MXFP8 only: E8M0 scales u8[m, ldxs], base and ldxs 4-byte aligned */
+    int64_t ldxs;
+    int64_t blocks;      /* K / 256 of this launch */
+    mambo_projection proj[MAMBO_MAX_GROUP];
+} mambo_chain_launch;
+typedef struct mambo_chain_config {
+    int32_t waves;               /* waves per workgroup: 4, 8 or 16 (0: 4) */
+    int32_t tiles_per_workgroup; /* 16-row weight tiles each workgroup takes (0: 1) */
+    int64_t timeout_us;          /* bound of each dependency wait, at most 60 s (0: 2 s) */
+    int32_t wait_bias;           /* tests only: added to every wait's target, so waits time out */
+    int32_t reserved[3];
+} mambo_chain_config;
+int mambo_iq3s_fp8_matmul_chain(int64_t m, const mambo_chain_launch *launches, int count,
+                                const mambo_chain_config *cfg, uint32_t *sync, mambo_stream_t stream);
+
+/* Reads the status of the chained calls that used `sync` (synchronously: it waits for the
+ * device copy). MAMBO_ERR_RUNTIME when a dependency wait timed out (all sync words are then
+ * cleared: after a timeout, launches may have finished out of order) or when the counters
+ * are not zero; else MAMBO_OK. */
+int mambo_chain_status(uint32_t *sync);
 
 /* The configuration mambo_iq3s_fp8_matmul uses when cfg == NULL. */
 int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out);

@@ -23,6 +23,7 @@ MAMBO_ERR_UNSUPPORTED = -4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_MXFP8 = 2
 
 GEMM_AUTO = 0
 GEMM_STREAM = 1
@@ -66,6 +67,25 @@ class Projection(ctypes.Structure):
     _fields_ = [("packed", ctypes.c_void_p), ("n", ctypes.c_int64), ("out", ctypes.c_void_p), ("ldo", ctypes.c_int64)]
 
 
+MAX_CHAIN = 16  # MAMBO_MAX_CHAIN
+CHAIN_SYNC_WORDS = 4224  # MAMBO_CHAIN_SYNC_WORDS
+
+
+class ChainLaunch(ctypes.Structure):
+    """mirror of mambo_chain_launch"""
+
+    _fields_ = [("x", ctypes.c_void_p), ("x_dtype", ctypes.c_int32), ("count", ctypes.c_int32),
+                ("ldx", ctypes.c_int64), ("xs", ctypes.c_void_p), ("ldxs", ctypes.c_int64),
+                ("blocks", ctypes.c_int64), ("proj", Projection * MAX_GROUP)]
+
+
+class ChainConfig(ctypes.Structure):
+    """mirror of mambo_chain_config"""
+
+    _fields_ = [("waves", ctypes.c_int32), ("tiles_per_workgroup", ctypes.c_int32), ("timeout_us", ctypes.c_int64),
+                ("wait_bias", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
+
+
 # name -> (restype, argtypes); every symbol here is declared in include/mambo_hip.h.
 _vp, _i64, _i32, _u64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint64
 SIGNATURES = {
@@ -87,6 +107,9 @@ SIGNATURES = {
                                              ctypes.POINTER(GemmConfig), _vp]),
     "mambo_iq3s_matmul_quantize_grouped": (_i32, [_vp, _i32, _i64, _i64, ctypes.POINTER(Projection), _i32, _i64,
                                                   ctypes.POINTER(GemmConfig), _vp, _i64, _vp, _i64, _vp]),
+    "mambo_iq3s_fp8_matmul_chain": (_i32, [_i64, ctypes.POINTER(ChainLaunch), _i32, ctypes.POINTER(ChainConfig),
+                                           _vp, _vp]),
+    "mambo_chain_status": (_i32, [_vp]),
     "mambo_gemm_default_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_gemm_check_config": (_i32, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig)]),
     "mambo_gemm_config_enumerate": (_i64, [_i64, _i64, _i64, ctypes.POINTER(GemmConfig), _i64]),

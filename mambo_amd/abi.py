@@ -46,6 +46,7 @@ _SCALARS = {
     "uint8_t": "uint8", "uint16_t": "uint16", "uint32_t": "uint32", "uint64_t": "uint64",
     "float": "float32", "double": "float64", "mambo_gemm_config": "mambo_gemm_config",
     "mambo_projection": "mambo_projection", "mambo_stream_t": "hipStream_t",
+    "mambo_chain_launch": "mambo_chain_launch", "mambo_chain_config": "mambo_chain_config",
 }
 
 
@@ -156,6 +157,12 @@ CONSTRAINTS: dict[str, list[dict]] = {
         _arr("xv", "uint8", ["m", "blocks*256"], ["ldxv", "1"], align=16, access="write"),
         _arr("xs", "uint8", ["m", "blocks*8"], ["ldxs", "1"], access="write"),
     ],
+    "mambo_iq3s_fp8_matmul_chain": [
+        _arr("launches", "mambo_chain_launch", ["count"], align=8, memory="host"),
+        _arr("cfg", "mambo_chain_config", ["1"], align=8, memory="host", nullable=True),
+        _arr("sync", "uint32", ["MAMBO_CHAIN_SYNC_WORDS"], align=4, access="readwrite"),
+    ],
+    "mambo_chain_status": [_arr("sync", "uint32", ["MAMBO_CHAIN_SYNC_WORDS"], align=4, access="readwrite")],
     "mambo_gemm_default_config": [_arr("out", "mambo_gemm_config", ["1"], align=4, memory="host", access="write")],
     "mambo_gemm_check_config": [_arr("cfg", "mambo_gemm_config", ["1"], align=4, memory="host")],
     "mambo_gemm_config_enumerate": [

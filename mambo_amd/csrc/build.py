@@ -25,7 +25,7 @@ LOADTEST = PKG / "mambo_loadtest"
 BUILD_DIR = CSRC / "_build"
 ARCH = "gfx950"
 
-SOURCES = ["api.hip", "quantize_mxfp8.hip", "iq3s_layout.hip", "iq3s_gemm.hip", "synth.hip"]
+SOURCES = ["api.hip", "quantize_mxfp8.hip", "iq3s_layout.hip", "iq3s_gemm.hip", "iq3s_chain.hip", "synth.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -285,6 +285,8 @@ MAMBO_ABI_NAME(float, "float32")
 MAMBO_ABI_NAME(double, "float64")
 MAMBO_ABI_NAME(mambo_gemm_config, "mambo_gemm_config")
 MAMBO_ABI_NAME(mambo_projection, "mambo_projection")
+MAMBO_ABI_NAME(mambo_chain_launch, "mambo_chain_launch")
+MAMBO_ABI_NAME(mambo_chain_config, "mambo_chain_config")
 MAMBO_ABI_NAME(mambo_stream_t, "hipStream_t")
 #undef MAMBO_ABI_NAME
 template <class T> struct AbiName<T *> {
@@ -339,6 +341,8 @@ const std::vector<EntryDecl> &compiled_entries()
                     "stream"),
         MAMBO_ENTRY(mambo_iq3s_matmul_quantize_grouped, "x", "x_dtype", "ldx", "m", "proj", "count", "blocks", "cfg",
                     "xv", "ldxv", "xs", "ldxs", "stream"),
+        MAMBO_ENTRY(mambo_iq3s_fp8_matmul_chain, "m", "launches", "count", "cfg", "sync", "stream"),
+        MAMBO_ENTRY(mambo_chain_status, "sync"),
         MAMBO_ENTRY(mambo_gemm_default_config, "m", "n", "blocks", "out"),
         MAMBO_ENTRY(mambo_gemm_check_config, "m", "n", "blocks", "cfg"),
         MAMBO_ENTRY(mambo_gemm_config_enumerate, "m", "n", "blocks", "out", "capacity"),
@@ -416,7 +420,7 @@ struct Manifest {
 
 const std::set<std::string> kDtypes = {"uint8",  "uint16",  "uint32",           "int32",
                                        "float32", "char",   "float32|bfloat16", "mambo_gemm_config",
-                                       "mambo_projection"};
+                                       "mambo_projection", "mambo_chain_launch", "mambo_chain_config"};
 
 void validate_constraint(const Json &c, const std::map<std::string, std::string> &pointer_types)
 {

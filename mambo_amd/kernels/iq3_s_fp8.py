@@ -21,6 +21,7 @@ weights uses scale d * (1 + 2 * scale_nibble).
 from __future__ import annotations
 
 import json
+from dataclasses import dataclass, field
 from functools import lru_cache
 from pathlib import Path
 
@@ -297,6 +298,108 @@ def launch_iq3_s_matmul_quantize(x: torch.Tensor, iq3_weights, *, stream=None, c
             xv.data_ptr(), xv.stride(0), xs.data_ptr(), xs.stride(0), _native.stream_handle(stream)),
             "launch_iq3_s_matmul_quantize")
     return result[0] if single else result
+
+
+@dataclass
+class ChainLaunch:
+    """One launch of a chained call (launch_iq3_s_fp8_matmul_chain): 1..4 weights with the
+    same K applied to the same activations. ``x``: uint8 [M, K] E4M3 values with
+    ``x_scales`` uint8 [M, K/32] E8M0, or float32 / bfloat16 [M, K] rows (quantized to
+    MXFP8 inside the kernel, as launch_quantize_fp8 would) - for instance the output of an
+    earlier launch of the same chain. ``outs``: optional float32 [M, N_i] outputs."""
+
+    x: torch.Tensor
+    weights: list
+    x_scales: torch.Tensor | None = None
+    outs: list | None = field(default=None)
+
+
+def new_chain_sync(device=None) -> torch.Tensor:
+    """Zeroed sync words for chained calls (MAMBO_CHAIN_SYNC_WORDS int32). Calls ordered on
+    one stream may share them (each call leaves them zero); calls that may overlap need
+    their own."""
+    return torch.zeros(_native.CHAIN_SYNC_WORDS, dtype=torch.int32, device=device or "cuda")
+
+
+def chain_status(sync: torch.Tensor) -> None:
+    """Raise RuntimeError if a chained call on ``sync`` had a dependency wait time out
+    (synchronises with the device; clears the reported status)."""
+    with torch.cuda.device(sync.device):
+        _native.check(_native.lib().mambo_chain_status(sync.data_ptr()), "chain_status")
+
+
+def launch_iq3_s_fp8_matmul_chain(launches, *, stream=None, waves: int = 0, sync: torch.Tensor | None = None,
+                                  timeout_us: int = 0, tiles_per_workgroup: int = 0, wait_bias: int = 0) -> list:
+    """Up to MAX_CHAIN launches at 1..4 tokens in one kernel launch, in order (no
+    reference counterpart: the reference calls launch_iq3_s_fp8_matmul per weight,
+    iq3_s_fp8.py:364-399). Returns, per launch, the list of its float32 [M, N_i] outputs:
+    what launch_iq3_s_fp8_matmul_grouped returns for each launch run one after the other
+    on the stream (bit-identical with the same ``waves``, 4, 8 or 16; 0 = the library's).
+    Launch i reads its activations only after every output of the launches before it is
+    stored, so a launch may take an earlier launch's output as its float32 input.
+    ``sync``: zeroed sync words (new_chain_sync), reusable by calls ordered on one stream;
+    default: fresh ones per call. ``timeout_us``, ``tiles_per_workgroup``, ``wait_bias``:
+    see mambo_chain_config (wait_bias is for tests that force a timeout; check with
+    chain_status)."""
+    launches = list(launches)
+    if not 1 <= len(launches) <= _native.MAX_CHAIN:
+        raise ValueError(f"between 1 and {_native.MAX_CHAIN} launches per chained call")
+    dtypes = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16}
+    descs = (_native.ChainLaunch * len(launches))()
+    results, m, dev = [], None, None
+    for i, cl in enumerate(launches):
+        if not isinstance(cl, ChainLaunch):
+            raise TypeError("launches must be ChainLaunch objects")
+        weights = list(cl.weights)
+        if not 1 <= len(weights) <= _native.MAX_GROUP:
+            raise ValueError(f"launch {i}: between 1 and {_native.MAX_GROUP} weights")
+        dims = [_weight_dimensions(w) for w in weights]
+        k_blocks = dims[0][1]
+        if any(b != k_blocks for _, b in dims):
+            raise ValueError(f"launch {i}: weights must share K")
+        k = k_blocks * IQ3_S_BLOCK_VALUES
+        x = cl.x
+        if not isinstance(x, torch.Tensor) or x.ndim != 2 or x.shape[0] < 1 or x.shape[1] != k:
+            raise ValueError(f"launch {i}: x must be [M,{k}]")
+        if m is None:
+            m, dev = int(x.shape[0]), x.device
+        if int(x.shape[0]) != m or x.device != dev:
+            raise ValueError("every launch of a chain takes the same M tokens on the same device")
+        desc = descs[i]
+        if x.dtype == torch.uint8:
+            x, xs, _ = _prepare_activations(x, cl.x_scales, k)  # rows 16- and 8-byte aligned
+            desc.x_dtype, desc.xs, desc.ldxs = _native.DTYPE_MXFP8, xs.data_ptr(), xs.stride(0)
+        elif x.dtype in dtypes:
+            if cl.x_scales is not None:
+                raise ValueError(f"launch {i}: x_scales belongs to MXFP8 (uint8) activations")
+            esz = x.element_size()
+            if x.stride(1) != 1 or x.data_ptr() % 16 or (x.stride(0) * esz) % 16:
+                x = x.contiguous() if x.data_ptr() % 16 == 0 else x.clone()
+            desc.x_dtype, desc.xs, desc.ldxs = dtypes[x.dtype], None, 0
+        else:
+            raise ValueError(f"launch {i}: x must be uint8 (MXFP8), float32 or bfloat16, got {x.dtype}")
+        if cl.outs is not None and len(cl.outs) != len(weights):
+            raise ValueError(f"launch {i}: outs must hold one output per weight")
+        with torch.cuda.device(dev):
+            outs = [_output(None if cl.outs is None else cl.outs[j], m, n, dev) for j, (n, _) in enumerate(dims)]
+            for j, (w, (n, _)) in enumerate(zip(weights, dims)):
+                desc.proj[j] = _native.Projection(ensure_packed(w, stream).data_ptr(), n, outs[j].data_ptr(),
+                                                  outs[j].stride(0))
+        desc.x, desc.ldx, desc.count, desc.blocks = x.data_ptr(), x.stride(0), len(weights), k_blocks
+        results.append((outs, x))
+    cfg = _native.ChainConfig()
+    cfg.waves, cfg.tiles_per_workgroup, cfg.timeout_us, cfg.wait_bias = waves, tiles_per_workgroup, timeout_us, \
+        wait_bias
+    with torch.cuda.device(dev):
+        if sync is None:
+            sync = new_chain_sync(dev)
+        if sync.dtype not in (torch.int32, torch.uint32) or sync.numel() < _native.CHAIN_SYNC_WORDS \
+                or not sync.is_contiguous() or sync.device != dev:
+            raise ValueError(f"sync must be {_native.CHAIN_SYNC_WORDS} contiguous int32 words on the device")
+        _native.check(_native.lib().mambo_iq3s_fp8_matmul_chain(m, descs, len(launches), cfg, sync.data_ptr(),
+                                                                _native.stream_handle(stream)),
+                      "launch_iq3_s_fp8_matmul_chain")
+    return [outs for outs, _ in results]
 
 
 def gemm_search_space(m: int, n: int, k: int) -> list[dict]:

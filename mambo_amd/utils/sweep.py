@@ -114,13 +114,63 @@ def launch_shape(projs) -> tuple[int, int]:
     return sum(n for n, _, _, _ in projs), projs[0][1]
 
 
-def make_step(launches, configs: Sequence[dict], with_quant: str = "none") -> Callable[[], None]:
+def make_step(launches, configs: Sequence[dict], with_quant: str = "none", chain: int = 0,
+              chain_waves: int = 0, chain_tpw: int = 0) -> Callable[[], None]:
     """One step: every launch with its configuration. with_quant: "none" (MXFP8 rows
     prepared beforehand), "separate" (a quantizer launch before each GEMM) or "fused"
-    (the rows quantized inside the GEMM)."""
-    from mambo_amd.kernels.iq3_s_fp8 import (launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped,
-                                             launch_iq3_s_matmul_quantize)
+    (the rows quantized inside the GEMM). chain > 0 (1..4 tokens): consecutive runs of
+    `chain` launches go to launch_iq3_s_fp8_matmul_chain as one persistent launch each,
+    every launch still reading its activations only after the one before it has stored
+    all its outputs (configs are then unused; chain_waves: 4, 8 or 16, chain_tpw: tiles per
+    workgroup, 0 = the library's);
+    "fused" hands the chain the bf16 rows, which it quantizes in the kernel."""
+    from mambo_amd.kernels.iq3_s_fp8 import (ChainLaunch, launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_chain,
+                                             launch_iq3_s_fp8_matmul_grouped, launch_iq3_s_matmul_quantize,
+                                             new_chain_sync)
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
+
+    if chain:
+        if with_quant == "separate":
+            raise ValueError("a chain quantizes inside the kernel (with_quant fused) or takes MXFP8 rows (none)")
+        descs = []
+        for _, projs, (xv, xs, rows) in launches:
+            if with_quant == "fused":
+                descs.append(ChainLaunch(rows, [p[2] for p in projs], outs=[p[3] for p in projs]))
+            else:
+                descs.append(ChainLaunch(xv, [p[2] for p in projs], x_scales=xs, outs=[p[3] for p in projs]))
+        # runs of consecutive launches with the same K, at most `chain` each: the chained
+        # kernel's LDS holds the rows of its longest K for every workgroup, so a long-K launch
+        # (the down projection) would cut the residency of all the others; it runs alone
+        chunks, i = [], 0
+        while i < len(descs):
+            j = i + 1
+            k = launches[i][1][0][1]
+            while j < len(descs) and j - i < chain and launches[j][1][0][1] == k:
+                j += 1
+            chunks.append((i, j))
+            i = j
+        sync = new_chain_sync()  # the chained calls are ordered on one stream: one set of words
+
+        def chained():
+            for i, j in chunks:
+                if j - i == 1:
+                    single_launch(i)
+                else:
+                    launch_iq3_s_fp8_matmul_chain(descs[i:j], waves=chain_waves, tiles_per_workgroup=chain_tpw,
+                                                  sync=sync)
+
+        def single_launch(i):
+            (_, projs, (xv, xs, rows)), cfg = launches[i], configs[i]
+            if with_quant == "fused":
+                launch_iq3_s_matmul_quantize(rows, [p[2] for p in projs], config=cfg, outs=[p[3] for p in projs])
+            elif len(projs) == 1:
+                launch_iq3_s_fp8_matmul(xv, xs, projs[0][2], config=cfg, out=projs[0][3])
+            else:
+                launch_iq3_s_fp8_matmul_grouped(xv, xs, [p[2] for p in projs], config=cfg,
+                                                outs=[p[3] for p in projs])
+
+        chained.sync = sync
+        return chained
 
     def step():
         for (_, projs, (xv, xs, rows)), cfg in zip(launches, configs):

@@ -246,3 +246,37 @@ def test_split_table_is_exact():
             hi, lo = Fraction(float(dec[hb])) * 2, Fraction(float(dec[lb])) * 2
             assert hb < 0x80 and hi == rne4(p), (s, lvl, hb, hi)
             assert hi + lo == p and abs(lo) <= 16, (s, lvl, hi, lo)
+
+
+def test_chain_validation_without_gpu():
+    """mambo_iq3s_fp8_matmul_chain rejects bad arguments before touching the device."""
+    from mambo_amd import _native
+    lib = _native.lib()
+    sync = (ctypes.c_uint32 * _native.CHAIN_SYNC_WORDS)()
+    one = (_native.ChainLaunch * 1)()
+    one[0].x, one[0].x_dtype, one[0].count, one[0].ldx = 16, _native.DTYPE_MXFP8, 1, 256
+    one[0].xs, one[0].ldxs, one[0].blocks = 16, 8, 1
+    one[0].proj[0] = _native.Projection(16, 16, 16, 16)
+    sp = ctypes.addressof(sync)
+    cases = [
+        (lambda: lib.mambo_iq3s_fp8_matmul_chain(1, one, 0, None, sp, None), "count must be in"),
+        (lambda: lib.mambo_iq3s_fp8_matmul_chain(5, one, 1, None, sp, None), "1..4 tokens"),
+        (lambda: lib.mambo_iq3s_fp8_matmul_chain(1, one, 1, None, None, None), "null pointer"),
+    ]
+    for call, text in cases:
+        assert call() == _native.MAMBO_ERR_VALUE
+        assert text in lib.mambo_last_error().decode()
+    for field, value, text in (("x_dtype", 7, "x_dtype"), ("ldx", 100, "row stride"), ("blocks", 0, "K blocks"),
+                               ("count", 5, "count must be in"), ("xs", 17, "4-byte aligned")):
+        bad = (_native.ChainLaunch * 1)()
+        ctypes.pointer(bad[0])[0] = one[0]
+        setattr(bad[0], field, value)
+        assert lib.mambo_iq3s_fp8_matmul_chain(1, bad, 1, None, sp, None) == _native.MAMBO_ERR_VALUE, field
+        assert text in lib.mambo_last_error().decode(), (field, lib.mambo_last_error())
+    cfg = _native.ChainConfig()
+    cfg.waves = 6
+    assert lib.mambo_iq3s_fp8_matmul_chain(1, one, 1, cfg, sp, None) == _native.MAMBO_ERR_VALUE
+    assert "waves" in lib.mambo_last_error().decode()
+    cfg.waves, cfg.tiles_per_workgroup = 4, -1
+    assert lib.mambo_iq3s_fp8_matmul_chain(1, one, 1, cfg, sp, None) == _native.MAMBO_ERR_VALUE
+    assert "tiles per workgroup" in lib.mambo_last_error().decode()

@@ -168,11 +168,11 @@ def test_usage_errors_exit_2():
 def test_constraint_expressions_use_only_parameters(manifests):
     """Every shape and stride expression evaluates to a positive integer from the
     entry point's own integer parameters (sample values) and the library's
-    mambo_iq3s_packed_bytes / MAMBO_READ_SINK_WORDS."""
+    mambo_iq3s_packed_bytes / MAMBO_READ_SINK_WORDS / MAMBO_CHAIN_SYNC_WORDS."""
     from mambo_amd import _native
     lib = _native.lib()
     env = {"mambo_iq3s_packed_bytes": lambda n, b: lib.mambo_iq3s_packed_bytes(n, b),
-           "MAMBO_READ_SINK_WORDS": _native.READ_SINK_WORDS}
+           "MAMBO_READ_SINK_WORDS": _native.READ_SINK_WORDS, "MAMBO_CHAIN_SYNC_WORDS": _native.CHAIN_SYNC_WORDS}
     for sym, doc in manifests.items():
         ints = {p["name"]: 64 for p in doc["parameters"] if not p["type"].endswith("*")
                 and p["type"] in ("int32", "int64", "uint64")}
