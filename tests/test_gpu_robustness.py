@@ -103,7 +103,8 @@ def test_release_soa_fields_on_the_gpu(gpu):
     release_soa_fields(fields)
     torch.cuda.synchronize()
     assert not has_soa_fields(fields)
-    assert before - torch.cuda.memory_allocated(gpu) >= raw.nbytes
+    # the five placeholders each take one 512-byte block of torch's caching allocator
+    assert before - torch.cuda.memory_allocated(gpu) >= raw.nbytes - 5 * 512
     step("projection after the release")
     second = launch_iq3_s_fp8_matmul(xvg, xsg, fields)
     torch.cuda.synchronize()
