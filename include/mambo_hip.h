@@ -228,6 +228,21 @@ int mambo_iq3s_fp8_matmul_chain(int64_t m, const mambo_chain_launch *launches, i
  * are not zero; else MAMBO_OK. */
 int mambo_chain_status(uint32_t *sync);
 
+/* mambo_iq3s_matmul_quantize_grouped without the caller's MXFP8 buffers: allocates
+ * nothing (no hipMalloc, no allocating library call). No reference counterpart; for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it). Where the rows are not quantized inside the GEMM (M > 4,
+ * unaligned rows, rows too long for LDS) their MXFP8 form is staged in a device array
+ * the library holds once per GPU (MAMBO_NOALLOC_SCRATCH_BYTES, until the process ends):
+ * calls needing more than that (m*K + m*K/32 bytes, K = blocks*256) return
+ * MAMBO_ERR_VALUE. Every call on a GPU shares that GPU's array, so calls that overlap in
+ * time on one GPU (on different streams) race; calls ordered on one stream do not. The
+ * results equal mambo_iq3s_matmul_quantize_grouped's with the same cfg. */
+#define MAMBO_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int mambo_iq3s_matmul_quantize_grouped_noalloc(const void *x, int x_dtype, int64_t ldx, int64_t m,
+                                               const mambo_projection *proj, int count, int64_t blocks,
+                                               const mambo_gemm_config *cfg, mambo_stream_t stream);
+
 /* The configuration mambo_iq3s_fp8_matmul uses when cfg == NULL. */
 int mambo_gemm_default_config(int64_t m, int64_t n, int64_t blocks, mambo_gemm_config *out);
 

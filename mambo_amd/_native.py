@@ -69,6 +69,7 @@ class Projection(ctypes.Structure):
 
 MAX_CHAIN = 16  # MAMBO_MAX_CHAIN
 CHAIN_SYNC_WORDS = 4224  # MAMBO_CHAIN_SYNC_WORDS
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # MAMBO_NOALLOC_SCRATCH_BYTES
 
 
 class ChainLaunch(ctypes.Structure):
@@ -107,6 +108,8 @@ SIGNATURES = {
                                              ctypes.POINTER(GemmConfig), _vp]),
     "mambo_iq3s_matmul_quantize_grouped": (_i32, [_vp, _i32, _i64, _i64, ctypes.POINTER(Projection), _i32, _i64,
                                                   ctypes.POINTER(GemmConfig), _vp, _i64, _vp, _i64, _vp]),
+    "mambo_iq3s_matmul_quantize_grouped_noalloc": (_i32, [_vp, _i32, _i64, _i64, ctypes.POINTER(Projection), _i32,
+                                                          _i64, ctypes.POINTER(GemmConfig), _vp]),
     "mambo_iq3s_fp8_matmul_chain": (_i32, [_i64, ctypes.POINTER(ChainLaunch), _i32, ctypes.POINTER(ChainConfig),
                                            _vp, _vp]),
     "mambo_chain_status": (_i32, [_vp]),

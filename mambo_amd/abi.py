@@ -157,6 +157,11 @@ CONSTRAINTS: dict[str, list[dict]] = {
         _arr("xv", "uint8", ["m", "blocks*256"], ["ldxv", "1"], align=16, access="write"),
         _arr("xs", "uint8", ["m", "blocks*8"], ["ldxs", "1"], access="write"),
     ],
+    "mambo_iq3s_matmul_quantize_grouped_noalloc": [
+        _arr("x", "float32|bfloat16", ["m", "blocks*256"], ["ldx", "1"], align=2),
+        _arr("proj", "mambo_projection", ["count"], align=8, memory="host"),
+        _arr("cfg", "mambo_gemm_config", ["1"], align=4, memory="host", nullable=True),
+    ],
     "mambo_iq3s_fp8_matmul_chain": [
         _arr("launches", "mambo_chain_launch", ["count"], align=8, memory="host"),
         _arr("cfg", "mambo_chain_config", ["1"], align=8, memory="host", nullable=True),

@@ -26,6 +26,8 @@
 // partial dot product of exactly the group lane l decoded, so each lane post-scales its
 // own accumulator by its own group's F; the four g' partials are summed at the end.
 // M up to 4 per MFMA, up to 16 per pass (U = 1..4 MFMAs per K step).
+#include <mutex>
+
 #include "iq3s_stream.h"
 
 namespace {
@@ -2035,4 +2037,70 @@ extern "C" int mambo_iq3s_matmul_quantize_grouped(const void *x, int x_dtype, in
     if (qrc)
         return qrc;
     return run_projections(xv, ldxv, xs, ldxs, m, proj, count, blocks, cfg, s);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// Staging array of mambo_iq3s_matmul_quantize_grouped_noalloc: the MXFP8 rows of a call
+// whose rows are not quantized inside the GEMM (values [m, K] at offset 0, scales
+// [m, K/32] at the next 256-byte boundary). One copy per GPU, held until the process
+// ends. Host code never passes the array's name: it is a host-side stand-in, and each
+// GPU holds its own copy at its own address, which hipGetSymbolAddress gives per device.
+namespace {
+static __device__ __align__(256) uint8_t scratch[MAMBO_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device (with that device
+// current) and kept.
+int scratch_address(uint8_t **out)
+{
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess)
+        return mambo_fail(MAMBO_ERR_RUNTIME, "hipGetDevice: %s", hipGetErrorString(err));
+    MAMBO_REQUIRE(dev >= 0 && dev < kMaxDevices, MAMBO_ERR_UNSUPPORTED, "device %d beyond the library's %d", dev,
+                  kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || ptr == nullptr)
+            return mambo_fail(MAMBO_ERR_RUNTIME, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                              hipGetErrorString(err));
+        g_scratch_ptr[dev] = static_cast<uint8_t *>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return MAMBO_OK;
+}
+} // namespace
+
+extern "C" int mambo_iq3s_matmul_quantize_grouped_noalloc(const void *x, int x_dtype, int64_t ldx, int64_t m,
+                                                          const mambo_projection *proj, int count, int64_t blocks,
+                                                          const mambo_gemm_config *cfg, mambo_stream_t stream)
+{
+    MAMBO_REQUIRE(x_dtype == MAMBO_DTYPE_F32 || x_dtype == MAMBO_DTYPE_BF16, MAMBO_ERR_VALUE,
+                  "activation dtype must be float32 or bfloat16");
+    MAMBO_REQUIRE(x, MAMBO_ERR_VALUE, "null pointer");
+    MAMBO_REQUIRE(m >= 1 && blocks >= 1 && blocks <= (1 << 20), MAMBO_ERR_VALUE, "shape must be positive");
+    const int64_t k = blocks * 256;
+    const int64_t xs_off = (m * k + 255) / 256 * 256;
+    MAMBO_REQUIRE(m <= MAMBO_NOALLOC_SCRATCH_BYTES / k && xs_off + m * (k / 32) <= MAMBO_NOALLOC_SCRATCH_BYTES,
+                  MAMBO_ERR_VALUE,
+                  "noalloc: %lld rows of K=%lld need %lld bytes of MXFP8 staging, beyond the library's %d",
+                  (long long)m, (long long)k, (long long)(xs_off + m * (k / 32)), MAMBO_NOALLOC_SCRATCH_BYTES);
+    uint8_t *ptr = nullptr;
+    int rc = scratch_address(&ptr);
+    if (rc)
+        return rc;
+    const hipStream_t s = (hipStream_t)stream;
+    rc = run_projections(reinterpret_cast<const uint8_t *>(x), ldx, nullptr, 0, m, proj, count, blocks, cfg, s,
+                         x_dtype);
+    if (rc != kNotFused)
+        return rc;
+    rc = mambo_quantize_mxfp8(x, x_dtype, m, k, ldx, ptr, k, ptr + xs_off, k / 32, stream);
+    if (rc)
+        return rc;
+    return run_projections(ptr, k, ptr + xs_off, k / 32, m, proj, count, blocks, cfg, s);
 }

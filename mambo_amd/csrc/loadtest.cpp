@@ -341,6 +341,8 @@ const std::vector<EntryDecl> &compiled_entries()
                     "stream"),
         MAMBO_ENTRY(mambo_iq3s_matmul_quantize_grouped, "x", "x_dtype", "ldx", "m", "proj", "count", "blocks", "cfg",
                     "xv", "ldxv", "xs", "ldxs", "stream"),
+        MAMBO_ENTRY(mambo_iq3s_matmul_quantize_grouped_noalloc, "x", "x_dtype", "ldx", "m", "proj", "count", "blocks",
+                    "cfg", "stream"),
         MAMBO_ENTRY(mambo_iq3s_fp8_matmul_chain, "m", "launches", "count", "cfg", "sync", "stream"),
         MAMBO_ENTRY(mambo_chain_status, "sync"),
         MAMBO_ENTRY(mambo_gemm_default_config, "m", "n", "blocks", "out"),
