@@ -405,10 +405,13 @@ def roofline_of(r: dict, mfma_bound: bool, workload: str) -> dict:
 
 
 # Further points of the M = 1..8192 metric timed by the default run, after the headline:
-# the Llama-3-70B sweep at 16, 32 and 512 tokens (same weights), then the Llama-3-8B
-# sweep at the decode sizes 1, 4 and 16 and the prefill sizes 2048 and 8192 (32 layers,
-# 3.0 GB of weights built beside the 70B ones).
-DEFAULT_POINTS = "llama70b:16,llama70b:32,llama70b:512,llama8b:1,llama8b:4,llama8b:16,llama8b:2048,llama8b:8192"
+# the Llama-3-70B sweep at 16, 32 and 512 tokens (same weights), and at 1 token with one
+# launch per projection (":nogroup", the way a caller of the reference's
+# launch_iq3_s_fp8_matmul runs a layer, iq3_s_fp8.py:364-399); then the Llama-3-8B sweep
+# at the decode sizes 1, 4 and 16 (1 also one launch per projection) and the prefill sizes
+# 2048 and 8192 (32 layers, 3.0 GB of weights built beside the 70B ones).
+DEFAULT_POINTS = ("llama70b:16,llama70b:32,llama70b:512,llama70b:1:nogroup,llama8b:1,llama8b:4,llama8b:16,"
+                  "llama8b:1:nogroup,llama8b:2048,llama8b:8192")
 
 
 def sweep_points(args, held: dict) -> list:
@@ -428,14 +431,18 @@ def sweep_points(args, held: dict) -> list:
         return []
     out = []
     for item in spec.split(","):
-        wl, m = item.split(":")
+        wl, m, *flags = item.split(":")
         sub = _ap.Namespace(**vars(args))
         sub.workload, sub.m = wl, int(m)
+        if flags:
+            if flags != ["nogroup"]:
+                raise ValueError(f"point {item}: the only flag is nogroup")
+            sub.no_group = True
         sub.layers = 80 if wl == "llama70b" else 32
         key = (sub.workload, sub.layers, sub.tp)
         if key not in held:
             held[key] = build_weights(sub.workload, sub.layers, sub.tp)
-        log(f"point {wl} M={m}")
+        log(f"point {item}")
         r = run_gemm(sub, held[key])
         mfma_bound = sub.m >= PREFILL_M
         name = gemm_workload_name(sub)
@@ -471,7 +478,7 @@ def main(argv=None) -> int:
     p.add_argument("--chain-waves", type=int, default=0, help="waves per workgroup of the chained launches")
     p.add_argument("--chain-tpw", type=int, default=0, help="16-row tiles per workgroup of the chained launches")
     p.add_argument("--points", default="auto",
-                   help="further workload:m points timed after the headline, comma-separated, or 'none' "
+                   help="further workload:m[:nogroup] points timed after the headline, comma-separated, or 'none' "
                         f"(auto: {DEFAULT_POINTS} when the headline is the default 70B M=1 sweep)")
     p.add_argument("--tp", type=int, default=1,
                    help="sweep one GPU's shard of a tensor-parallel layer: N/tp rows of q/k/v and gate/up, "
