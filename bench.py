@@ -381,8 +381,8 @@ def gemm_workload_name(args) -> str:
         grouping += {"separate": ", a quantizer launch before each GEMM launch",
                      "fused": ", quantization inside the GEMM launch where it fits (M <= 4)"}[args.with_quant]
     if getattr(args, "chain", 0):
-        grouping += (f", {args.chain} consecutive launches per persistent chained launch (each launch's "
-                     "activation reads wait for the one before it)")
+        grouping += (f", runs of up to {args.chain} consecutive launches of one K per chained launch (each "
+                     "launch's activation reads wait for the one before it)")
     model = "llama3-70b" if args.workload == "llama70b" else "llama3-8b"
     shard = f" (one GPU's shard at tensor parallelism {args.tp})" if args.tp > 1 else ""
     return f"{model} projection sweep{shard}: {args.layers} layers x 7 IQ3_S linears, M={args.m}, {grouping}"
@@ -396,6 +396,7 @@ def roofline_of(r: dict, mfma_bound: bool, workload: str) -> dict:
         return {"bound": "mfma", "achieved": round(value, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(value / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic(workload),
                 "algorithmic_flops_per_launch": round(r["step_flops"] / r["launches"]),
+                "algorithmic_operand_bytes_per_launch": round(r["per_launch_bytes"]),
                 "avg_launch_us": round(r["per_launch_us"], 3)}
     value = r["value"]
     return {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -448,6 +449,7 @@ def sweep_points(args, held: dict) -> list:
         name = gemm_workload_name(sub)
         out.append({"workload": name, "m": sub.m, "value": round(r["tflops"] if mfma_bound else r["value"], 2),
                     "unit": "TFLOP/s" if mfma_bound else "GB/s", "ms_per_step": round(r["ms"], 4),
+                    "launches_per_step": r["launches"],
                     "gbs": round(r["value"], 2), "tflops": round(r["tflops"], 3),
                     "roofline": roofline_of(r, mfma_bound, name)})
     return out

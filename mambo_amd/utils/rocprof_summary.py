@@ -16,6 +16,11 @@ Two reports, both plain text meant to be committed next to the numbers they back
   MFMA flops against the algorithmic ones. The CSV's ``GRBM_GUI_ACTIVE`` is the sum over
   the XCDs (MfmaUtil's formula takes the maximum), so the busy fraction divides by the
   per-XCD mean.
+* ``points``: the same three figures for every point of one ``bench.py`` run (the headline
+  and its ``points`` list, read from the JSON line the run printed): the kernel trace, the
+  ``FETCH_SIZE`` / ``WRITE_SIZE`` runs and the MFMA counter run of the bench command are
+  each cut into the points' steps (see ``segment_points``), and one Markdown table plus one
+  traffic record per point (read by ``bench.py`` for ``roofline.traffic``) are written.
 * ``traffic``: HBM bytes per dispatch from two ``--pmc`` runs (``FETCH_SIZE``, then
   ``WRITE_SIZE``) of a workload, each scaled by what the same counter reads for the plain
   copy kernel (``mambo_copy_bytes``) over a known number of bytes in two more runs. The
@@ -180,6 +185,207 @@ def window_report(args) -> None:
     print("\n".join(lines))
 
 
+# Kernels a projection step dispatches: the GEMM families and the K split's output fill.
+STEP_KERNELS = ("gemm_", "zero_rows_kernel")
+
+
+def _is_step(name: str) -> bool:
+    return any(k in name for k in STEP_KERNELS)
+
+
+def bench_points(bench_json: str) -> list[dict]:
+    """The headline and the points of a bench.py JSON line, in the order the run timed them:
+    workload, m, launches per step, ms per step, algorithmic work per launch and unit."""
+    line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
+    out = [{"workload": line["config"]["workload"], "m": line["config"]["m"],
+            "launches": line["config"]["launches_per_step"], "ms_per_step": line["ms_per_step"],
+            "roofline": line["roofline"], "value": line["value"], "unit": line["unit"]}]
+    for p in line.get("points", []):
+        out.append({"workload": p["workload"], "m": p["m"], "launches": p["launches_per_step"],
+                    "ms_per_step": p["ms_per_step"], "roofline": p["roofline"], "value": p["value"],
+                    "unit": p["unit"]})
+    return out, line["steps"], line["warmup"]
+
+
+def step_runs(names: list[str]) -> list[tuple[int, int]]:
+    """[start, end) index ranges of the maximal runs of consecutive step dispatches."""
+    runs, i = [], 0
+    while i < len(names):
+        if _is_step(names[i]):
+            j = i
+            while j < len(names) and _is_step(names[j]):
+                j += 1
+            runs.append((i, j))
+            i = j
+        else:
+            i += 1
+    return runs
+
+
+def segment_points(names: list[str], points: list[dict], steps_per_run: int, window_steps: int) -> list[range]:
+    """Per point, the dispatch indices of its last `window_steps` steps. A point's steps end
+    in a run of step dispatches that nothing else interrupts, of a length that is
+    `steps_per_run` times the point's dispatches per step (its launches plus any K-split
+    fills: between 1x and 2x its launches). The points take such runs in order. In
+    bench.py's graph mode the run is the warm-up and timed replays (W + K steps: the eager
+    step and the check replay are each followed by other kernels); in its eager mode at
+    --steps 1 --warmup 0 it is the eager step and the timed one (2 steps)."""
+    runs = step_runs(names)
+    out, r = [], 0
+    for p in points:
+        while r < len(runs):
+            a, b = runs[r]
+            r += 1
+            n = b - a
+            if n % steps_per_run == 0 and p["launches"] <= n // steps_per_run <= 2 * p["launches"]:
+                d = n // steps_per_run
+                out.append(range(b - window_steps * d, b))
+                break
+        else:
+            raise ValueError(f"no run of steps for point {p['workload']}")
+    return out
+
+
+def _work_per_step(p: dict) -> tuple[float, str]:
+    roof = p["roofline"]
+    if roof["unit"] == "TFLOP/s":
+        return roof["algorithmic_flops_per_launch"] * p["launches"], "flops"
+    return roof["algorithmic_bytes_per_launch"] * p["launches"], "bytes"
+
+
+def points_report(args) -> None:
+    points, steps, warmup = bench_points(args.bench_json)
+    lines = [f"# Every point of one bench run: kernel trace, HBM traffic, MFMA counters", "",
+             "Bench line: `" + args.bench_command + "` (its JSON line is the source of the points, their steps "
+             "and launches).", "", "Points, in the order the run times them, and their workload strings:", ""]
+    lines += [f"* {_label(p)}: `{p['workload']}`" for p in points] + [""]
+    rec_out = []
+    trace = kernel_trace(args.trace) if args.trace else None
+    plain = bench_points(args.plain_json)[0] if args.plain_json else None
+    if plain is not None and [q["workload"] for q in plain] != [p["workload"] for p in points]:
+        raise ValueError("the plain run's points differ from the traced run's")
+    if trace is not None:
+        names = [r["name"] for r in trace]
+        windows = segment_points(names, points, warmup + steps, steps)
+        lines += ["## Kernel trace (timed replays of each point)", "", "Commands (the plain run first, then the "
+                  "traced one, on one box):", "", "```", args.plain_command, args.trace_command, "```", "",
+                  "Per point, the last `steps` replays of its run of graph replays in the trace. GEMM us per "
+                  "launch = the step's `gemm_*` kernel durations over its launches; kernel ms per step = every "
+                  "dispatch of the step (GEMMs and K-split output fills) summed; frac (kernel) = the step's "
+                  "algorithmic work over that kernel time, against the peak. Bench figures are HIP events around "
+                  "the same replays: in the traced run (the tracer adds ~2 us between short graph kernels) and "
+                  "in the plain run before it. The trace backs the plain line when its kernel time per step is "
+                  "at most the plain ms per step. Under the tracer a K-split output fill (and even an empty "
+                  "kernel) shows ~4.5 us, against ~1.8 us per fill in an untraced graph replay, so at the points "
+                  "with fills the GEMM time per step is the figure to hold against the plain line.", "",
+                  "| point | dispatches/step | GEMM us/launch | bench us/launch (traced) | bench us/launch (plain) "
+                  "| GEMM ms/step | kernel ms/step | bench ms/step (plain) | frac (kernel) | frac (plain) |",
+                  "|---|---|---|---|---|---|---|---|---|---|"]
+        for k, (p, win) in enumerate(zip(points, windows)):
+            rows = [trace[i] for i in win]
+            kernel_ns = sum(r["end"] - r["start"] for r in rows)
+            gemm = [r["end"] - r["start"] for r in rows if "gemm_" in r["name"]]
+            work, unit = _work_per_step(p)
+            kern_ms = kernel_ns / steps / 1e6
+            peak = 5000.0 if unit == "flops" else 8000.0
+            scale = 1e12 if unit == "flops" else 1e9
+            frac_kernel = work / (kern_ms * 1e-3) / scale / peak
+            q = plain[k] if plain is not None else None
+            lines.append(f"| {_label(p)} | {len(rows) // steps} | {sum(gemm) / len(gemm) / 1e3:.3f} | "
+                         f"{p['roofline']['avg_launch_us']:.3f} | "
+                         f"{'-' if q is None else format(q['roofline']['avg_launch_us'], '.3f')} | "
+                         f"{sum(gemm) / steps / 1e6:.4f} | {kern_ms:.4f} | "
+                         f"{'-' if q is None else format(q['ms_per_step'], '.4f')} | {frac_kernel:.4f} | "
+                         f"{'-' if q is None else format(q['roofline']['frac'], '.4f')} |")
+            rec_out.append({"workload": p["workload"], "dispatches_per_step": len(rows) // steps,
+                            "gemm_us_per_launch": sum(gemm) / len(gemm) / 1e3,
+                            "gemm_ms_per_step": sum(gemm) / steps / 1e6, "kernel_ms_per_step": kern_ms,
+                            "frac_kernel": frac_kernel, "traced_bench_ms_per_step": p["ms_per_step"],
+                            "plain_bench_ms_per_step": None if q is None else q["ms_per_step"],
+                            "plain_frac": None if q is None else q["roofline"]["frac"]})
+    if args.fetch and args.write:
+        cal_fetch = sum(counter_per_dispatch(args.calib_fetch, "FETCH_SIZE", args.calib_family)) / \
+            len(counter_per_dispatch(args.calib_fetch, "FETCH_SIZE", args.calib_family))
+        cal_write = sum(counter_per_dispatch(args.calib_write, "WRITE_SIZE", args.calib_family)) / \
+            len(counter_per_dispatch(args.calib_write, "WRITE_SIZE", args.calib_family))
+        f_factor, w_factor = args.copy_bytes / cal_fetch, args.copy_bytes / cal_write
+        fetch = counter_rows(args.fetch, "FETCH_SIZE")
+        write = counter_rows(args.write, "WRITE_SIZE")
+        fw = segment_points([r[0] for r in fetch], points, 2, 1)
+        ww = segment_points([r[0] for r in write], points, 2, 1)
+        lines += ["", "## HBM traffic (one eager step of each point, every dispatch of the step)", "", "Commands:", "",
+                  "```", args.traffic_command, "```", "",
+                  f"Counters scaled by the copy calibration: FETCH_SIZE {f_factor:.1f} and WRITE_SIZE "
+                  f"{w_factor:.1f} bytes per unit (`mambo_copy_bytes` over {args.copy_bytes:,} bytes).", "",
+                  "| point | dispatches | traffic per launch | algorithmic per launch | ratio |", "|---|---|---|---|---|"]
+        for p, fr, wr in zip(points, fw, ww):
+            fb = sum(fetch[i][1] for i in fr) * f_factor
+            wb = sum(write[i][1] for i in wr) * w_factor
+            per_launch = (fb + wb) / p["launches"]
+            roof = p["roofline"]
+            algo = roof.get("algorithmic_bytes_per_launch")
+            if algo is None:  # MFMA-bound points: bytes of the projections' operands
+                algo = roof.get("algorithmic_operand_bytes_per_launch")
+            ratio = per_launch / algo if algo else None
+            lines.append(f"| {_label(p)} | {len(fr)} | {per_launch:,.0f} | "
+                         f"{'-' if algo is None else f'{algo:,.0f}'} | {'-' if ratio is None else f'{ratio:.3f}'} |")
+            rec = {"workload": p["workload"], "kernel_family": "gemm_ + zero_rows_kernel (whole step)",
+                   "dispatches": len(fr), "calibration": {"copy_bytes": args.copy_bytes, "fetch_size": cal_fetch,
+                                                          "write_size": cal_write, "fetch_bytes_per_unit": f_factor,
+                                                          "write_bytes_per_unit": w_factor},
+                   "fetch_bytes_per_launch": fb / p["launches"], "write_bytes_per_launch": wb / p["launches"],
+                   "traffic_bytes_per_launch": per_launch, "algorithmic_bytes_per_launch": algo,
+                   "traffic_over_algorithmic": ratio, "command": args.traffic_command}
+            slug = _slug(p)
+            Path(args.out_dir, f"traffic_{slug}.json").write_text(json.dumps(rec, indent=1) + "\n")
+    if args.mfma:
+        busy = counter_rows(args.mfma, "SQ_VALU_MFMA_BUSY_CYCLES")
+        mops = counter_rows(args.mfma, "SQ_INSTS_VALU_MFMA_MOPS_F8")
+        gui = counter_rows(args.mfma, "GRBM_GUI_ACTIVE")
+        bw = segment_points([r[0] for r in busy], points, 2, 1)
+        lines += ["", "## MFMA counters (one eager step of each MFMA-bound point)", "", "Command:", "", "```",
+                  args.mfma_command, "```", "",
+                  f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {args.xcds} XCDs x "
+                  f"{args.cus * SIMD_PER_CU} SIMDs), over the step's tiled-kernel dispatches weighted by their "
+                  "active cycles; executed F8 flops = SQ_INSTS_VALU_MFMA_MOPS_F8 x 512.", "",
+                  "| point | MFMA busy | executed / algorithmic F8 flops |", "|---|---|---|"]
+        simds = args.cus * SIMD_PER_CU
+        for p, win in zip(points, bw):
+            if p["roofline"]["unit"] != "TFLOP/s":
+                continue
+            b = sum(busy[i][1] for i in win)
+            g = sum(gui[i][1] for i in win)
+            m = sum(mops[i][1] for i in win)
+            work, _ = _work_per_step(p)
+            lines.append(f"| {_label(p)} | {100 * b / (g / args.xcds * simds):.1f}% | {m * 512 / work:.3f} |")
+    Path(args.out).write_text("\n".join(lines) + "\n")
+    if rec_out:
+        Path(args.out).with_suffix(".json").write_text(json.dumps(rec_out, indent=1) + "\n")
+    print("\n".join(lines))
+
+
+def _label(p: dict) -> str:
+    return (f"{'70B' if '70b' in p['workload'] else '8B'} M={p['m']}"
+            f"{' (one launch per projection)' if 'one launch per' in p['workload'] else ''}")
+
+
+def _slug(p: dict) -> str:
+    model = "llama70b" if "70b" in p["workload"] else "llama8b"
+    tail = "_nogroup" if "one launch per projection" in p["workload"] else ""
+    return f"{model}_m{p['m']}{tail}"
+
+
+def counter_rows(directory: str, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, value) of `counter` for every dispatch of a --pmc run, in dispatch order."""
+    rows = []
+    with open(_one(directory, "_counter_collection.csv"), newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(n, v) for _, n, v in rows]
+
+
 SIMD_PER_CU = 4
 
 
@@ -246,6 +452,26 @@ def main(argv=None) -> int:
     w.add_argument("--note", default="the timed replays")
     w.add_argument("--command", required=True)
     w.add_argument("--out", required=True)
+    q = sub.add_parser("points")
+    q.add_argument("--bench-json", required=True)
+    q.add_argument("--bench-command", required=True)
+    q.add_argument("--plain-json", default="")
+    q.add_argument("--plain-command", default="")
+    q.add_argument("--trace", default="")
+    q.add_argument("--trace-command", default="")
+    q.add_argument("--fetch", default="")
+    q.add_argument("--write", default="")
+    q.add_argument("--calib-fetch", default="")
+    q.add_argument("--calib-write", default="")
+    q.add_argument("--calib-family", default="copy_bytes_kernel")
+    q.add_argument("--copy-bytes", type=int, default=1 << 30)
+    q.add_argument("--traffic-command", default="")
+    q.add_argument("--mfma", default="")
+    q.add_argument("--mfma-command", default="")
+    q.add_argument("--cus", type=int, default=256)
+    q.add_argument("--xcds", type=int, default=8)
+    q.add_argument("--out", required=True)
+    q.add_argument("--out-dir", default="profiles")
     m = sub.add_parser("mfma")
     m.add_argument("dir")
     m.add_argument("--family", required=True)
@@ -256,7 +482,8 @@ def main(argv=None) -> int:
     for name in ("--workload", "--command", "--out"):
         m.add_argument(name, required=True)
     args = p.parse_args(argv)
-    {"stats": stats_report, "traffic": traffic_report, "window": window_report, "mfma": mfma_report}[args.cmd](args)
+    {"stats": stats_report, "traffic": traffic_report, "window": window_report, "mfma": mfma_report,
+     "points": points_report}[args.cmd](args)
     return 0
 
 

@@ -34,3 +34,23 @@ def test_shard_that_breaks_a_tile_or_block_is_refused():
         layer_shapes("llama8b", 3)
     with pytest.raises(ValueError, match="down: K=28672 does not split into 32 shards of whole 256-weight blocks"):
         layer_shapes("llama70b", 32)
+
+
+def test_profile_segmentation_finds_each_points_timed_steps():
+    """The per-point profile summary cuts a kernel trace into the points' timed steps: runs
+    of GEMM / K-split fill dispatches that other kernels (input set-up, copies, checks)
+    separate. A point whose K-split adds a fill per launch has up to twice its launches."""
+    from mambo_amd.utils.rocprof_summary import segment_points
+
+    def step(launches, fills):
+        return ["gemm_stream_kernel"] * launches + ["zero_rows_kernel"] * fills
+
+    names = ["randn"] + step(3, 0) + ["copy"] + step(3, 0) + ["allclose"]  # eager step, check replay
+    names += step(3, 0) * 4 + ["randn"]                                      # W=2 + K=2 replays
+    names += step(2, 2) + ["copy"] + step(2, 2) + ["allclose"] + step(2, 2) * 4
+    points = [{"workload": "a", "launches": 3}, {"workload": "b", "launches": 2}]
+    a, b = segment_points(names, points, 4, 2)
+    assert [names[i] for i in a] == step(3, 0) * 2 and a.stop == names.index("randn", 1)
+    assert [names[i] for i in b] == step(2, 2) * 2 and b.stop == len(names)
+    with pytest.raises(ValueError, match="no run of steps for point c"):
+        segment_points(names, points + [{"workload": "c", "launches": 1}], 4, 2)
