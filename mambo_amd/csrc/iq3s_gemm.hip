@@ -771,22 +771,30 @@ __device__ __forceinline__ void mfma_half(const uint8_t *buf, const uint32_t (&a
     }
 }
 
-template <int MT, int NT, int W, bool kHalf = false>
+// kKs > 1 (16- and 32-token tiles): the W waves form kKs groups of W/kKs that take the
+// workgroup's K blocks in turn (group g: blocks b0+g, b0+g+kKs, ...), each group staging
+// its own block per step, so a workgroup of the same weight rows holds kKs times the
+// waves; the groups' sums are added through LDS in group order at the end.
+template <int MT, int NT, int W, bool kHalf = false, int kKs = 1>
 __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
 {
     constexpr int kRows = TiledBlock<MT>::kRows;
     constexpr int kThreads = W * 64;
+    constexpr int kTw = W / kKs; // waves of one K group (one per NT weight tiles)
+    static_assert(W % kKs == 0 && (kKs == 1 || !kHalf), "K groups");
     // a 16-token tile reads each weight once per launch: stream it (non-temporal), as the
     // decode kernels do; larger token tiles re-read it once per token tile
     constexpr int kPolicy = MT == 1 ? kStreamPolicy : 0;
-    __shared__ __align__(16) uint8_t s_buf0[TiledBlock<MT>::kBytes];
-    __shared__ __align__(16) uint8_t s_buf1[TiledBlock<MT>::kBytes];
+    __shared__ __align__(16) uint8_t s_buf0[kKs * TiledBlock<MT>::kBytes];
+    __shared__ __align__(16) uint8_t s_buf1[kKs * TiledBlock<MT>::kBytes];
     __shared__ uint32_t s_lvl[512];
     __shared__ uint4 s_split[16];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = kKs == 1 ? 0 : wave_all / kTw;  // K group
+    const int wave = wave_all - kg * kTw;           // wave within the group
     const int col = lane & 15, q = lane >> 4;
 
     // this workgroup's projection; tile_begin counts workgroups here
@@ -809,7 +817,7 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     int64_t tile[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        tile[nt] = wg * (NT * W) + wave * NT + nt;
+        tile[nt] = wg * (NT * kTw) + wave * NT + nt;
         wt[nt] = byte_rsrc(packed + min(tile[nt], tiles - 1) * (int64_t)B * kTileBytes);
     }
 
@@ -841,28 +849,34 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
                 acc[mt][nt][r] = 0.0f;
 
     // K range of this workgroup: blocks [b0, b1) (grid z splits K; partial sums are
-    // added into an output zeroed beforehand)
+    // added into an output zeroed beforehand). Step s: K group kg takes block
+    // b0 + s*kKs + kg (clamped for its loads; no math past b1).
     const uint8_t *lvl = reinterpret_cast<const uint8_t *>(s_lvl);
     const int b0 = blockIdx.z * bps, b1 = min(B, b0 + bps);
     WTile wcur[NT], wnext[kHalf ? 1 : NT];
     v8i bh[kHalf ? 1 : NT][2], bl[kHalf ? 1 : NT][2]; // full-K form
     v8i hh[NT], hl[NT];                              // half-K form
     float d[NT];
+    constexpr int kBufStride = TiledBlock<MT>::kBytes;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-        wcur[nt] = load_w_rsrc<kPolicy>(wt[nt], (uint32_t)b0 * kTileBytes, lane, col);
-    stage_block<MT, W>(s_buf0, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, b0, wave, lane);
+        wcur[nt] = load_w_rsrc<kPolicy>(wt[nt], (uint32_t)min(b0 + kg, b1 - 1) * kTileBytes, lane, col);
+    stage_block<MT, kTw>(s_buf0 + kg * kBufStride, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row,
+                         min(b0 + kg, b1 - 1), wave, lane);
     __syncthreads();
 
     // Block b: copy block b+1's activations into the other buffer and request its weight
     // tiles, then decode block b's weights and run its MFMAs; the barrier at the end waits
     // for the copies (and frees this buffer for block b+2's). Two fixed buffers (the loop
     // is unrolled by two), so the compiler can tell the copy target from the buffer read.
-#define MAMBO_TILED_BLOCK(cur, nxt)                                                                                \
+    // (b: this K group's block of the step; b + kKs: its next one.)
+#define MAMBO_TILED_BLOCK(cur_, nxt_)                                                                              \
     do {                                                                                                           \
-        stage_block<MT, W>(nxt, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, min(b + 1, b1 - 1), wave,    \
-                           lane);                                                                                  \
-        const uint32_t next_ = (uint32_t)min(b + 1, b1 - 1) * kTileBytes;                                          \
+        uint8_t *cur = (cur_) + kg * kBufStride;                                                                   \
+        uint8_t *nxt = (nxt_) + kg * kBufStride;                                                                   \
+        stage_block<MT, kTw>(nxt, xrows, (uint32_t)ldxv, srows, (uint32_t)ldxs, last_row, min(b + kKs, b1 - 1),     \
+                             wave, lane);                                                                          \
+        const uint32_t next_ = (uint32_t)min(b + kKs, b1 - 1) * kTileBytes;                                        \
         if constexpr (kHalf) {                                                                                     \
             __builtin_amdgcn_sched_barrier(0);                                                                     \
             for (int nt = 0; nt < NT; ++nt)                                                                        \
@@ -877,20 +891,55 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
             for (int nt = 0; nt < NT; ++nt)                                                                        \
                 wnext[nt] = load_w_rsrc<kPolicy>(wt[nt], next_, lane, col);                                        \
             __builtin_amdgcn_sched_barrier(0);                                                                     \
-            decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);                                                       \
-            mfma_block<MT, NT>(cur, ao, soff, bh, bl, d, acc);                                                     \
+            if (kKs == 1 || b < b1) {                                                                              \
+                decode_tiles<NT>(wcur, lvl, s_split, bh, bl, d);                                                   \
+                mfma_block<MT, NT>(cur, ao, soff, bh, bl, d, acc);                                                 \
+            }                                                                                                      \
             for (int nt = 0; nt < NT; ++nt)                                                                        \
                 wcur[nt] = wnext[nt];                                                                              \
         }                                                                                                          \
         __syncthreads();                                                                                           \
     } while (0)
-    for (int b = b0; b < b1; ++b) {
+    // steps: the same count for every K group (a group past b1 only stages and waits)
+    const int b_end = b0 + (b1 - b0 + kKs - 1) / kKs * kKs;
+    for (int b = b0 + kg; b < b_end; b += kKs) {
         MAMBO_TILED_BLOCK(s_buf0, s_buf1);
-        if (++b == b1)
+        if ((b += kKs) >= b_end)
             break;
         MAMBO_TILED_BLOCK(s_buf1, s_buf0);
     }
 #undef MAMBO_TILED_BLOCK
+    if constexpr (kKs > 1) {
+        // groups 1.. hand their sums to group 0 through LDS (the loop's last barrier has
+        // retired every copy into the buffers); group 0 adds them in group order
+        constexpr int kE = MT * NT * 4;
+        static_assert((kKs - 1) * kTw * 64 * kE * 4 <= kKs * TiledBlock<MT>::kBytes, "reduction fits buffer 0");
+        float *red = reinterpret_cast<float *>(s_buf0);
+        if (kg > 0) {
+            float *dst = red + ((kg - 1) * kTw + wave) * 64 * kE + lane;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        dst[64 * ((mt * NT + nt) * 4 + r)] = acc[mt][nt][r];
+        }
+        __syncthreads();
+        if (kg > 0)
+            return;
+#pragma unroll
+        for (int g = 1; g < kKs; ++g) {
+            const float *src = red + ((g - 1) * kTw + wave) * 64 * kE + lane;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[mt][nt][r] += src[64 * ((mt * NT + nt) * 4 + r)];
+        }
+    }
 
     // D[i][j] of sub-tile (mt, nt): lane j + 16*(i/4), register i%4 -> token
     // m0 + 16*mt + 4q + r, weight row 16*tile + col.
@@ -1385,7 +1434,7 @@ int launch_dense(bool dry, int waves, int nt, int mc, bool lds_act, dim3 grid, s
     }
 }
 
-template <int MT, int NT, int W>
+template <int MT, int NT, int W, int KS>
 void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t ldxs,
                     int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
 {
@@ -1393,26 +1442,40 @@ void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ld
         MAMBO_LAUNCH((gemm_prefill_kernel<W>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs, ldxs, M, ga, B, bps,
                      atomic);
     else // direct copies; the 256-token tiles of 256 weight rows in the half-K form
-        MAMBO_LAUNCH((gemm_tiled_kernel<MT, NT, W, (MT >= 16)>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs,
+        MAMBO_LAUNCH((gemm_tiled_kernel<MT, NT, W, (MT >= 16), KS>), grid, dim3(W * 64), 0, stream, xv, ldxv, xs,
                            ldxs, M, ga, B, bps, atomic);
 }
 
-// Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves).
-int launch_tiled(bool dry, int mt, int nt, int waves, dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ldxv,
-                 const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps, int atomic)
+// K groups of a tiled configuration: the 16- and 32-token tiles are 4 waves of weight rows
+// per K group, so their `waves` beyond 4 are groups splitting the workgroup's K blocks
+// (all but the 32-token tile of 8 waves x 16 rows, tile_n = 128, which has one group);
+// the larger tiles have one group.
+int tiled_groups(const mambo_gemm_config &c)
 {
-#define MAMBO_T(A, C, D)                                                                                           \
-    if (mt == A && nt == C && waves == D) {                                                                        \
+    if (c.tile_m > 32 || c.waves <= 4 || (c.tile_m == 32 && c.waves == 8 && c.tile_n == 128))
+        return 1;
+    return c.waves / 4;
+}
+
+// Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves, K
+// groups).
+int launch_tiled(bool dry, int mt, int nt, int waves, int ks, dim3 grid, hipStream_t stream, const uint8_t *xv,
+                 int64_t ldxv, const uint8_t *xs, int64_t ldxs, int64_t M, const GroupArgs &ga, int B, int bps,
+                 int atomic)
+{
+#define MAMBO_T(A, C, D, E)                                                                                        \
+    if (mt == A && nt == C && waves == D && ks == E) {                                                             \
         if (!dry)                                                                                                  \
-            launch_tiled_t<A, C, D>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                      \
+            launch_tiled_t<A, C, D, E>(grid, stream, xv, ldxv, xs, ldxs, M, ga, B, bps, atomic);                   \
         return MAMBO_OK;                                                                                           \
     }
-    MAMBO_T(1, 1, 4) MAMBO_T(1, 2, 4) MAMBO_T(1, 4, 4) MAMBO_T(2, 1, 4) MAMBO_T(2, 2, 4) MAMBO_T(2, 1, 8)
-    MAMBO_T(16, 1, 16) MAMBO_T(16, 1, 8) MAMBO_T(8, 2, 8) MAMBO_T(8, 2, 4) MAMBO_T(8, 1, 8) MAMBO_T(8, 1, 4)
-    MAMBO_T(4, 2, 8) MAMBO_T(4, 2, 4) MAMBO_T(4, 1, 8) MAMBO_T(4, 1, 4)
+    MAMBO_T(1, 1, 4, 1) MAMBO_T(1, 2, 4, 1) MAMBO_T(1, 4, 4, 1) MAMBO_T(2, 1, 4, 1) MAMBO_T(2, 2, 4, 1)
+    MAMBO_T(2, 1, 8, 1) MAMBO_T(1, 1, 8, 2) MAMBO_T(1, 2, 8, 2) MAMBO_T(1, 1, 16, 4) MAMBO_T(2, 1, 8, 2)
+    MAMBO_T(16, 1, 16, 1) MAMBO_T(16, 1, 8, 1) MAMBO_T(8, 2, 8, 1) MAMBO_T(8, 2, 4, 1) MAMBO_T(8, 1, 8, 1)
+    MAMBO_T(8, 1, 4, 1) MAMBO_T(4, 2, 8, 1) MAMBO_T(4, 2, 4, 1) MAMBO_T(4, 1, 8, 1) MAMBO_T(4, 1, 4, 1)
 #undef MAMBO_T
     return mambo_fail(MAMBO_ERR_VALUE, "tiled kernel: no build for tile_m=%d, tile_n=%d, waves=%d", 16 * mt,
-                      16 * nt * waves, waves);
+                      16 * nt * waves / ks, waves);
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -1669,14 +1732,18 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
                   MAMBO_ERR_VALUE, "unsupported kernel family %d", cfg->kernel);
     if (cfg->kernel == MAMBO_GEMM_TILED && (cfg->tile_m == 16 || cfg->tile_m == 32)) {
         if (cfg->tile_m == 16)
-            MAMBO_REQUIRE(cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128 || cfg->tile_n == 256),
+            MAMBO_REQUIRE((cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128 || cfg->tile_n == 256)) ||
+                              (cfg->waves == 8 && (cfg->tile_n == 64 || cfg->tile_n == 128)) ||
+                              (cfg->waves == 16 && cfg->tile_n == 64),
                           MAMBO_ERR_VALUE, "tiled: tile_m=16 is built for 4 waves of 16, 32 or 64 weight rows (tile_n=64, "
-                                           "128 or 256)");
+                                           "128 or 256), with 2 K groups of them for 16 or 32 rows (8 waves, tile_n=64 or "
+                                           "128) or 4 K groups for 16 rows (16 waves, tile_n=64)");
         else
             MAMBO_REQUIRE((cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128)) ||
-                              (cfg->waves == 8 && cfg->tile_n == 128),
+                              (cfg->waves == 8 && (cfg->tile_n == 64 || cfg->tile_n == 128)),
                           MAMBO_ERR_VALUE, "tiled: tile_m=32 is built for 4 waves of 16 or 32 weight rows (tile_n=64 "
-                                           "or 128) or 8 waves of 16 (tile_n=128)");
+                                           "or 128), 8 waves of 16 (tile_n=128) or 2 K groups of 4 waves of 16 (8 "
+                                           "waves, tile_n=64)");
         MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                       "split_k must be in [1, K/256]");
         return MAMBO_OK;
@@ -1768,16 +1835,21 @@ extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blo
     }
     if (m > 4 && m <= 64) // 16-token tiles: four waves share each activation block through LDS
         for (const int32_t rows : {16, 32, 64})
-            for (const int32_t split : {1, 2, 4})
-                if (split <= blocks)
-                    add(MAMBO_GEMM_TILED, 4, split, 16, rows * 4);
-    if (m > 16 && m <= 64) // 32-token tiles
+            for (const int32_t groups : {1, 2, 4}) // K groups of four waves inside the workgroup
+                if ((groups == 1 || (groups == 2 && rows <= 32) || rows == 16) && groups <= blocks)
+                    for (const int32_t split : {1, 2, 4})
+                        if (split * groups <= blocks)
+                            add(MAMBO_GEMM_TILED, 4 * groups, split, 16, rows * 4);
+    if (m > 16 && m <= 64) // 32-token tiles (8 waves: of 16 rows, tile_n 128, or two K groups, tile_n 64)
         for (const int32_t waves : {4, 8})
             for (const int32_t rows : {16, 32})
                 if (waves == 4 || rows == 16)
                     for (const int32_t split : {1, 2, 4})
-                        if (split <= blocks)
+                        if (split <= blocks) {
                             add(MAMBO_GEMM_TILED, waves, split, 32, rows * waves);
+                            if (waves == 8 && split * 2 <= blocks)
+                                add(MAMBO_GEMM_TILED, waves, split, 32, rows * 4);
+                        }
     if (m >= 32) { // tokens x weight rows per wave x waves
         for (const int32_t tile_m : {64, 128, 256})
             for (const int32_t waves : {4, 8, 16})
@@ -1953,7 +2025,8 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
     std::function<int(bool)> launch;
     const char *what = "iq3s_fp8_matmul";
     if (c.kernel == MAMBO_GEMM_TILED) {
-        const int mt = c.tile_m / 16, nt = c.tile_n / (16 * c.waves);
+        const int ks = tiled_groups(c), tw = c.waves / ks;
+        const int mt = c.tile_m / 16, nt = c.tile_n / (16 * tw);
         MAMBO_REQUIRE((uintptr_t)xs % 8 == 0 && ldxs % 8 == 0, MAMBO_ERR_VALUE,
                       "tiled: x_scales base and row stride must be 8-byte aligned");
         // the staging copies address a token tile with 32-bit offsets
@@ -1964,13 +2037,14 @@ int run_projections(const uint8_t *xv, int64_t ldxv, const uint8_t *xs, int64_t 
         int64_t wgs = 0;
         for (int g = 0; g < count; ++g) {
             gt.tile_begin[g] = wgs;
-            wgs += cdiv(cdiv(ga.n[g], kTileRows), (int64_t)nt * c.waves);
+            wgs += cdiv(cdiv(ga.n[g], kTileRows), (int64_t)nt * tw);
         }
         const int64_t mtiles = cdiv(m, c.tile_m);
         MAMBO_REQUIRE(wgs <= 0x7FFFFFFF && mtiles <= 65535, MAMBO_ERR_VALUE, "shape too large for one launch");
         const dim3 grid((unsigned)wgs, (unsigned)mtiles, (unsigned)splits);
         launch = [=](bool dry) {
-            return launch_tiled(dry, mt, nt, c.waves, grid, s, xv, ldxv, xs, ldxs, m, gt, (int)blocks, bps, atomic);
+            return launch_tiled(dry, mt, nt, c.waves, ks, grid, s, xv, ldxv, xs, ldxs, m, gt, (int)blocks, bps,
+                                atomic);
         };
         what = "iq3s_fp8_matmul (tiled)";
     } else {
