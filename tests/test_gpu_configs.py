@@ -47,6 +47,15 @@ def sample_rows(n: int, count: int, seed: int) -> np.ndarray:
     return np.unique(np.concatenate([np.arange(16), np.arange(n - 16, n), rest]))
 
 
+def sample_every_tile(n: int, seed: int) -> np.ndarray:
+    """The first and last 16 indices plus one random index inside every block of 16 (a
+    weight tile along N, a token sub-tile along M)."""
+    rng = np.random.default_rng(seed)
+    tiles = (n + 15) // 16
+    picks = np.minimum(np.arange(tiles) * 16 + rng.integers(0, 16, tiles), n - 1)
+    return np.unique(np.concatenate([np.arange(min(16, n)), np.arange(max(0, n - 16), n), picks]))
+
+
 def oracle_rows(xv: torch.Tensor, xs: torch.Tensor, seed: int, k: int, rows: np.ndarray) -> np.ndarray:
     raw = np.concatenate([oracle.gen_iq3s(seed, 1, k // 256, row0=int(r)) for r in rows])
     return oracle.iq3s_fp8_matmul(xv.cpu().numpy(), xs.cpu().numpy(), raw, threads=oracle.default_threads())
@@ -77,21 +86,25 @@ def test_reference_cpu_case_m8_4096_full(gpu):
 @pytest.mark.parametrize("m", [2048, 8192])
 @pytest.mark.parametrize("n,k", LLAMA8B)
 def test_prefill_llama8b_shapes(gpu, n, k, m):
-    """Prefill projections, sampled output rows; the tuned table's configuration
-    (config None) and the library default (kernel 0)."""
+    """Prefill projections on the tuned table's configuration (config None) and the
+    library default (kernel 0). Checked against the oracle: one random output column in
+    every 16-row weight tile and one random token in every 16-token sub-tile (plus the
+    first and last 16 of each), so every MFMA tile of every workgroup holds checked
+    outputs, at a lane position that varies from tile to tile; every output finite."""
     from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul, select_config
     from mambo_amd.kernels.quantize_fp8 import launch_quantize_fp8
     seed = 100 + n // 1024 + k // 1024
     step(f"synth weight {n}x{k}")
     fields = _synth_weight(gpu, n, k, seed=seed)
     xq, xs = launch_quantize_fp8(_synth_act(gpu, m, k, seed=seed + 1))
-    rows = sample_rows(n, 16 if m == 8192 else 32, seed)
-    expected = oracle_rows(xq, xs, seed, k, rows)
+    rows = sample_every_tile(n, seed)
+    toks = torch.from_numpy(sample_every_tile(m, seed + 7)).to(gpu)
+    expected = oracle_rows(xq[toks], xs[toks], seed, k, rows)
     for cfg in (None, {"kernel": 0}):
         step(f"matmul M={m} {n}x{k} config={cfg or select_config(m, n, k)}")
         out = launch_iq3_s_fp8_matmul(xq, xs, fields, config=cfg)
         torch.cuda.synchronize()
-        got = columns(out, rows)
+        got = columns(out[toks], rows)
         check(got, expected, elementwise=False)
         assert bool(torch.isfinite(out).all())
 
@@ -126,7 +139,14 @@ def test_llama70b_layer_projections(gpu, m, tp):
             outs = launch_iq3_s_fp8_matmul_grouped(xv, xs, [w[5] for w in group], config=cfg)
         torch.cuda.synchronize()
         for (name, n, k, _, seed, _), out in zip(group, outs):
-            rows = sample_rows(n, min(n - 32, 32 if m == 512 else 96), seed)
+            if m == 512:
+                # one column in every 16-row weight tile, one token in every 16-token sub-tile
+                rows = sample_every_tile(n, seed)
+                toks = torch.from_numpy(sample_every_tile(m, seed + 7)).to(gpu)
+                step(f"oracle {name} M={m} ({len(rows)} rows x {len(toks)} tokens)")
+                check(columns(out[toks], rows), oracle_rows(xv[toks], xs[toks], seed, k, rows), elementwise=False)
+                continue
+            rows = sample_rows(n, min(n - 32, 96), seed)
             step(f"oracle {name} M={m} ({len(rows)} rows)")
             check(columns(out, rows), oracle_rows(xv, xs, seed, k, rows), elementwise=False)
 
