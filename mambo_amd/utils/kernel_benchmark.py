@@ -14,7 +14,7 @@ of the candidates; a tuned entry replaces it only when it is faster by ``min_gai
 
     python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --model M.gguf --weight-name NAME
     python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --synthetic 4096 4096 [--write-table]
-    python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --sweep llama70b --tokens 1 16 [--write-table]
+    python -m mambo_amd.utils.kernel_benchmark iq3_s_fp8 --sweep llama70b --tokens 1 16 [--no-group] [--write-table]
 
 ``--sweep`` tunes every launch shape of a Llama-3 projection sweep inside the sweep
 itself, replayed from a HIP graph, where the step time decides (sweep_tune).
@@ -234,7 +234,7 @@ def _rel_l2(out: torch.Tensor, ref: torch.Tensor) -> float:
 
 def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, tp: int = 1, steps: int = 10,
                warmup: int = 2, min_gain: float = 0.01, rounds: int = 2, rtol: float = 1e-4,
-               quiet: bool = False, progress: int = 10) -> list[TuneResult]:
+               quiet: bool = False, progress: int = 10, no_group: bool = False) -> list[TuneResult]:
     """Tune each launch shape of a model's projection sweep inside the sweep.
 
     For each token count, the sweep's launches (mambo_amd.utils.sweep) are replayed from
@@ -248,7 +248,9 @@ def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, 
     `min_gain` (a fraction of the step time) faster. tuner_us and default_us are step
     times; mean_us, batched_us and event_us time one launch of the shape alone with the
     reference's three timers. Unless quiet, a progress line (candidates done, failures,
-    the best so far) is printed every `progress` candidates of a shape (0: none)."""
+    the best so far) is printed every `progress` candidates of a shape (0: none).
+    no_group: one launch per projection, as a caller of launch_iq3_s_fp8_matmul runs a
+    layer (the shapes of k, v, gate and up alone), instead of q/k/v and gate/up grouped."""
     from mambo_amd.kernels.iq3_s_fp8 import default_config, gemm_search_space, select_config, tuned_key
     from mambo_amd.utils.sweep import MODELS, build_launches, build_weights, capture, launch_shape, make_step, \
         time_replays
@@ -263,7 +265,7 @@ def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, 
     stream = torch.cuda.current_stream()
     results = []
     for m in tokens:
-        launches = build_launches(weights, m)
+        launches = build_launches(weights, m, no_group)
         shapes = [launch_shape(projs) for _, projs, _ in launches]
         keys = list(dict.fromkeys(shapes))
         chosen = {key: select_config(m, *key) for key in keys}
@@ -320,7 +322,8 @@ def sweep_tune(model: str, tokens: Sequence[int], *, layers: int | None = None, 
             mean_us = _host_time(stream, one, drain_each=True)
             batched_us = _host_time(stream, one, drain_each=False)
             event_us = _time_events(stream, one, 20)
-            result = TuneResult(f"M={m} N={key[0]} K={key[1]} in the {model} sweep", tuned_key(*key, m), dict(best),
+            where = f"the {model} sweep{', one launch per projection' if no_group else ''}"
+            result = TuneResult(f"M={m} N={key[0]} K={key[1]} in {where}", tuned_key(*key, m), dict(best),
                                 mean_us, batched_us, event_us, tuner_us, successes, failures, default_us,
                                 dict(default))
             results.append(result)
@@ -370,6 +373,8 @@ def benchmark_main(argv: Sequence[str] | None = None) -> list[TuneResult]:
     parser.add_argument("--layers", type=int, help="layers of the --sweep (default: all of the model's)")
     parser.add_argument("--tp", type=int, default=1, help="--sweep one GPU's shard at this tensor parallelism")
     parser.add_argument("--steps", type=int, default=10, help="timed sweep replays per --sweep candidate")
+    parser.add_argument("--no-group", action="store_true",
+                        help="--sweep with one launch per projection (as launch_iq3_s_fp8_matmul callers run a layer)")
     parser.add_argument("--tokens", type=int, nargs="+", default=[4, 128], help="token counts M to tune")
     parser.add_argument("--write-table", action="store_true", help="store winners in the tuned table")
     parser.add_argument("--table", type=Path, help="tuned table to write (default: the one the launcher reads)")
@@ -387,7 +392,7 @@ def benchmark_main(argv: Sequence[str] | None = None) -> list[TuneResult]:
             parser.error("--sweep tunes iq3_s_fp8 from replayed graphs of its own synthetic weights")
         module = importlib.import_module(kernel_module)
         results = sweep_tune(args.sweep, args.tokens, layers=args.layers, tp=args.tp, steps=args.steps,
-                             min_gain=0.01 if args.min_gain is None else args.min_gain)
+                             min_gain=0.01 if args.min_gain is None else args.min_gain, no_group=args.no_group)
         if args.write_table:
             from mambo_amd import _native
             write_tuned_table(results, args.table or module.TUNED_PATH, _native.device_arch())
