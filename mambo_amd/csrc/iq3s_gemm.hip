@@ -1446,15 +1446,17 @@ void launch_tiled_t(dim3 grid, hipStream_t stream, const uint8_t *xv, int64_t ld
                            ldxs, M, ga, B, bps, atomic);
 }
 
-// K groups of a tiled configuration: the 16- and 32-token tiles are 4 waves of weight rows
-// per K group, so their `waves` beyond 4 are groups splitting the workgroup's K blocks
-// (all but the 32-token tile of 8 waves x 16 rows, tile_n = 128, which has one group);
-// the larger tiles have one group.
+// K groups of a tiled configuration: in the 16- and 32-token tiles a K group is the
+// waves that cover tile_n weight rows (4 waves of 16 * (tile_n / 64) rows for tile_n >= 64,
+// else tile_n / 16 waves of 16 rows), and `waves` beyond one group are further groups
+// splitting the workgroup's K blocks (all but the 32-token tile of 8 waves x 16 rows,
+// tile_n = 128, which is one group); the larger tiles have one group.
 int tiled_groups(const mambo_gemm_config &c)
 {
-    if (c.tile_m > 32 || c.waves <= 4 || (c.tile_m == 32 && c.waves == 8 && c.tile_n == 128))
+    if (c.tile_m > 32 || (c.tile_m == 32 && c.waves == 8 && c.tile_n == 128))
         return 1;
-    return c.waves / 4;
+    const int tw = c.tile_n >= 64 ? 4 : std::max(1, c.tile_n / 16);
+    return std::max(1, c.waves / tw);
 }
 
 // Tile shapes the tiled kernel is built for: (tokens, weight rows per wave / 16, waves, K
@@ -1471,6 +1473,8 @@ int launch_tiled(bool dry, int mt, int nt, int waves, int ks, dim3 grid, hipStre
     }
     MAMBO_T(1, 1, 4, 1) MAMBO_T(1, 2, 4, 1) MAMBO_T(1, 4, 4, 1) MAMBO_T(2, 1, 4, 1) MAMBO_T(2, 2, 4, 1)
     MAMBO_T(2, 1, 8, 1) MAMBO_T(1, 1, 8, 2) MAMBO_T(1, 2, 8, 2) MAMBO_T(1, 1, 16, 4) MAMBO_T(2, 1, 8, 2)
+    MAMBO_T(1, 1, 4, 4) MAMBO_T(1, 1, 4, 2) MAMBO_T(1, 1, 8, 8) MAMBO_T(1, 1, 8, 4) MAMBO_T(1, 1, 16, 16)
+    MAMBO_T(1, 1, 16, 8) MAMBO_T(2, 1, 8, 8) MAMBO_T(2, 1, 8, 4)
     MAMBO_T(16, 1, 16, 1) MAMBO_T(16, 1, 8, 1) MAMBO_T(8, 2, 8, 1) MAMBO_T(8, 2, 4, 1) MAMBO_T(8, 1, 8, 1)
     MAMBO_T(8, 1, 4, 1) MAMBO_T(4, 2, 8, 1) MAMBO_T(4, 2, 4, 1) MAMBO_T(4, 1, 8, 1) MAMBO_T(4, 1, 4, 1)
 #undef MAMBO_T
@@ -1734,16 +1738,20 @@ extern "C" int mambo_gemm_check_config(int64_t m, int64_t n, int64_t blocks, con
         if (cfg->tile_m == 16)
             MAMBO_REQUIRE((cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128 || cfg->tile_n == 256)) ||
                               (cfg->waves == 8 && (cfg->tile_n == 64 || cfg->tile_n == 128)) ||
-                              (cfg->waves == 16 && cfg->tile_n == 64),
+                              (cfg->waves == 16 && cfg->tile_n == 64) ||
+                              ((cfg->waves == 4 || cfg->waves == 8 || cfg->waves == 16) &&
+                               (cfg->tile_n == 16 || cfg->tile_n == 32)),
                           MAMBO_ERR_VALUE, "tiled: tile_m=16 is built for 4 waves of 16, 32 or 64 weight rows (tile_n=64, "
                                            "128 or 256), with 2 K groups of them for 16 or 32 rows (8 waves, tile_n=64 or "
-                                           "128) or 4 K groups for 16 rows (16 waves, tile_n=64)");
+                                           "128) or 4 K groups for 16 rows (16 waves, tile_n=64), and for K groups of 1 or "
+                                           "2 waves of 16 rows (tile_n=16 or 32) in 4, 8 or 16 waves");
         else
             MAMBO_REQUIRE((cfg->waves == 4 && (cfg->tile_n == 64 || cfg->tile_n == 128)) ||
-                              (cfg->waves == 8 && (cfg->tile_n == 64 || cfg->tile_n == 128)),
+                              (cfg->waves == 8 && (cfg->tile_n == 16 || cfg->tile_n == 32 || cfg->tile_n == 64 ||
+                                                   cfg->tile_n == 128)),
                           MAMBO_ERR_VALUE, "tiled: tile_m=32 is built for 4 waves of 16 or 32 weight rows (tile_n=64 "
-                                           "or 128), 8 waves of 16 (tile_n=128) or 2 K groups of 4 waves of 16 (8 "
-                                           "waves, tile_n=64)");
+                                           "or 128), 8 waves of 16 (tile_n=128) or K groups of 1, 2 or 4 waves of 16 "
+                                           "in 8 waves (tile_n=16, 32 or 64)");
         MAMBO_REQUIRE(cfg->split_k >= 1 && cfg->split_k <= blocks && cfg->split_k <= 65535, MAMBO_ERR_VALUE,
                       "split_k must be in [1, K/256]");
         return MAMBO_OK;
@@ -1833,22 +1841,31 @@ extern "C" int64_t mambo_gemm_config_enumerate(int64_t m, int64_t n, int64_t blo
             }
         }
     }
-    if (m > 4 && m <= 64) // 16-token tiles: four waves share each activation block through LDS
+    if (m > 4 && m <= 64) { // 16-token tiles: four waves share each activation block through LDS
         for (const int32_t rows : {16, 32, 64})
             for (const int32_t groups : {1, 2, 4}) // K groups of four waves inside the workgroup
                 if ((groups == 1 || (groups == 2 && rows <= 32) || rows == 16) && groups <= blocks)
                     for (const int32_t split : {1, 2, 4})
                         if (split * groups <= blocks)
                             add(MAMBO_GEMM_TILED, 4 * groups, split, 16, rows * 4);
-    if (m > 16 && m <= 64) // 32-token tiles (8 waves: of 16 rows, tile_n 128, or two K groups, tile_n 64)
+        // K groups of one or two waves of 16 rows (4, 8 or 16 waves)
+        for (const int32_t group_waves : {1, 2})
+            for (const int32_t waves : {4, 8, 16})
+                for (const int32_t split : {1, 2, 4})
+                    if (split * (waves / group_waves) <= blocks)
+                        add(MAMBO_GEMM_TILED, waves, split, 16, 16 * group_waves);
+    }
+    if (m > 16 && m <= 64) // 32-token tiles (8 waves: of 16 rows, tile_n 128, or K groups, tile_n 16-64)
         for (const int32_t waves : {4, 8})
             for (const int32_t rows : {16, 32})
                 if (waves == 4 || rows == 16)
                     for (const int32_t split : {1, 2, 4})
                         if (split <= blocks) {
                             add(MAMBO_GEMM_TILED, waves, split, 32, rows * waves);
-                            if (waves == 8 && split * 2 <= blocks)
-                                add(MAMBO_GEMM_TILED, waves, split, 32, rows * 4);
+                            if (waves == 8) // K groups of 4, 2 or 1 waves of 16 rows
+                                for (const int32_t tn : {64, 32, 16})
+                                    if (split * (8 * 16 / tn) <= blocks)
+                                        add(MAMBO_GEMM_TILED, waves, split, 32, tn);
                         }
     if (m >= 32) { // tokens x weight rows per wave x waves
         for (const int32_t tile_m : {64, 128, 256})

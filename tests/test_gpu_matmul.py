@@ -476,11 +476,11 @@ def test_default_32_token_tiles(gpu):
 
 @pytest.mark.parametrize("m", [7, 16, 23, 32])
 def test_tiled_k_groups(gpu, m):
-    """16- and 32-token tiles whose workgroups hold 2 or 4 K groups of four waves (each
-    group takes every 2nd / 4th K block, the groups' sums added in LDS at the end), on 7
-    K blocks (a K range that the groups do not divide evenly) and N=100 (a partial weight
-    tile), with no K split and with split_k=3 (ranges of 3, 3 and 1 blocks), against the
-    oracle."""
+    """16- and 32-token tiles whose workgroups hold 2 to 16 K groups of one, two or four
+    waves (each group takes every G-th K block, the groups' sums added in LDS at the end),
+    on 7 K blocks (a K range that the groups do not divide evenly, and groups with no
+    block at all) and N=100 (a partial weight tile), with no K split and with split_k=3
+    (ranges of 3, 3 and 1 blocks), against the oracle."""
     from mambo_amd import _native
     from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
@@ -491,7 +491,9 @@ def test_tiled_k_groups(gpu, m):
     xv, xs = oracle.quantize_mxfp8(x)
     expected = oracle.iq3s_fp8_matmul(xv, xs, raw)
     xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
-    shapes = [(16, 8, 64), (16, 8, 128), (16, 16, 64)] + ([(32, 8, 64)] if m > 16 else [])
+    shapes = [(16, 8, 64), (16, 8, 128), (16, 16, 64), (16, 4, 16), (16, 4, 32), (16, 8, 16), (16, 8, 32),
+              (16, 16, 16), (16, 16, 32)]
+    shapes += [(32, 8, 64), (32, 8, 32), (32, 8, 16)] if m > 16 else []
     for tile_m, waves, tile_n in shapes:
         for split in (1, 3):
             cfg = {"kernel": _native.GEMM_TILED, "waves": waves, "split_k": split, "tile_m": tile_m,
