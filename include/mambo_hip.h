@@ -64,7 +64,8 @@ typedef struct mambo_gemm_config {
     int32_t waves;   /* waves (64 lanes) per workgroup */
     int32_t split_k; /* workgroups sharing one output tile along K (f32 atomics) */
     int32_t tile_m;  /* TILED: rows of M per workgroup */
-    int32_t tile_n;  /* TILED: rows of N per workgroup */
+    int32_t tile_n;  /* TILED: rows of N per workgroup (16/32-token tiles: per K group of waves;
+                        waves beyond one group split the workgroup's K blocks) */
     int32_t reserved[3];
 } mambo_gemm_config;
 
