@@ -393,11 +393,13 @@ def roofline_of(r: dict, mfma_bound: bool, workload: str) -> dict:
     average launch time over the timed region (HIP events on the launch stream)."""
     if mfma_bound:
         value = r["tflops"]
-        return {"bound": "mfma", "achieved": round(value, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+        roof = {"bound": "mfma", "achieved": round(value, 2), "peak": MXFP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(value / MXFP8_PEAK_TFLOPS, 4), "traffic": measured_traffic(workload),
                 "algorithmic_flops_per_launch": round(r["step_flops"] / r["launches"]),
-                "algorithmic_operand_bytes_per_launch": round(r["per_launch_bytes"]),
                 "avg_launch_us": round(r["per_launch_us"], 3)}
+        if "per_launch_bytes" in r:  # the projections' operand bytes (not for the MFMA-rate check)
+            roof["algorithmic_operand_bytes_per_launch"] = round(r["per_launch_bytes"])
+        return roof
     value = r["value"]
     return {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload),
