@@ -189,9 +189,9 @@ def test_end_to_end_against_unquantized_input(gpu, m):
 
 @pytest.mark.parametrize("m", [9, 16, 24, 33])
 def test_grouped_launch_through_16_and_32_token_tiles(gpu, m):
-    """Grouped projections (ragged N = 100, 37, 64) through every 16- and 32-token tile
-    the tiled kernel is built for, with and without a K split: each output is bit-
-    identical to its own launch under the same configuration and matches the oracle."""
+    """Grouped projections (ragged N = 100, 37, 64) through the 16- and 32-token tiles,
+    K groups included, with and without a K split: each output is bit-identical to its
+    own launch under the same configuration and matches the oracle."""
     from mambo_amd import _native
     from mambo_amd.kernels.iq3_s_fp8 import launch_iq3_s_fp8_matmul, launch_iq3_s_fp8_matmul_grouped
     from mambo_amd.utils.iq3_s_weight import prepare_iq3_s_fields
@@ -202,11 +202,14 @@ def test_grouped_launch_through_16_and_32_token_tiles(gpu, m):
     xv, xs = oracle.quantize_mxfp8(x)
     xvg, xsg = torch.from_numpy(xv).to(gpu), torch.from_numpy(xs).to(gpu)
     expected = [oracle.iq3s_fp8_matmul(xv, xs, r) for r in raws]
-    tiles = [(16, 4, 16), (16, 4, 32), (16, 4, 64), (32, 4, 16), (32, 4, 32), (32, 8, 16)]
-    for tile_m, waves, rows in tiles:
+    # (tokens, waves, tile_n): one group of four waves of 16/32/64 rows, 8 waves of 16 rows
+    # (32 tokens), and K groups of four, two or one waves (8 or 16 waves)
+    tiles = [(16, 4, 64), (16, 4, 128), (16, 4, 256), (32, 4, 64), (32, 4, 128), (32, 8, 128),
+             (16, 8, 64), (16, 16, 16), (16, 8, 32), (32, 8, 64), (32, 8, 16)]
+    for tile_m, waves, tile_n in tiles:
         for split in (1, 2):
             cfg = {"kernel": _native.GEMM_TILED, "waves": waves, "split_k": split, "tile_m": tile_m,
-                   "tile_n": rows * waves}
+                   "tile_n": tile_n}
             step(f"grouped tiled M={m} cfg={cfg}")
             outs = launch_iq3_s_fp8_matmul_grouped(xvg, xsg, fields, config=cfg)
             singles = [launch_iq3_s_fp8_matmul(xvg, xsg, f, config=cfg) for f in fields]
