@@ -230,7 +230,8 @@ def manifests(library_path: str = "../libmambo_hip.so", toolchain: dict | None =
 
 
 def write_manifests(out_dir: Path = ABI_DIR, library_path: str | None = None) -> list[Path]:
-    """Write ``<symbol>.abi.json`` for every entry point into out_dir."""
+    """Write ``<symbol>.abi.json`` for every entry point into out_dir, and remove the
+    manifests of symbols the library no longer exports."""
     out_dir = Path(out_dir)
     out_dir.mkdir(parents=True, exist_ok=True)
     if library_path is None:
@@ -240,6 +241,8 @@ def write_manifests(out_dir: Path = ABI_DIR, library_path: str | None = None) ->
         path = out_dir / f"{doc['symbol']}.abi.json"
         path.write_text(json.dumps(doc, indent=2, sort_keys=True) + "\n", encoding="utf-8")
         paths.append(path)
+    for stale in set(out_dir.glob("*.abi.json")) - set(paths):
+        stale.unlink()
     return paths
 
 

@@ -47,6 +47,15 @@ def test_one_manifest_per_declared_entry_point(manifests):
     assert abi.ABI_VERSION == 100
 
 
+def test_writing_removes_manifests_of_symbols_no_longer_exported(tmp_path):
+    from mambo_amd import abi
+    stale = tmp_path / "mambo_removed_entry_point.abi.json"
+    stale.write_text("{}\n")
+    written = abi.write_manifests(tmp_path)
+    assert not stale.exists()
+    assert sorted(p.name for p in tmp_path.iterdir()) == sorted(p.name for p in written)
+
+
 def test_loader_declarations_equal_the_header_parse(manifests):
     """The loader derives parameter types from the compiled declarations (decltype);
     the Python side parses the header text. Both must read the same ABI."""
