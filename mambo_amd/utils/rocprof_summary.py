@@ -193,9 +193,10 @@ def _is_step(name: str) -> bool:
     return any(k in name for k in STEP_KERNELS)
 
 
-def bench_points(bench_json: str) -> list[dict]:
-    """The headline and the points of a bench.py JSON line, in the order the run timed them:
-    workload, m, launches per step, ms per step, algorithmic work per launch and unit."""
+def bench_points(bench_json: str) -> tuple[list[dict], int, int]:
+    """(points, steps, warmup) of a bench.py JSON line: the headline and its points in
+    the order the run timed them (workload, m, launches per step, ms per step, roofline
+    object, value and unit each), and the run's timed and warm-up steps."""
     line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
     out = [{"workload": line["config"]["workload"], "m": line["config"]["m"],
             "launches": line["config"]["launches_per_step"], "ms_per_step": line["ms_per_step"],
