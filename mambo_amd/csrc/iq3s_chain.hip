@@ -249,15 +249,17 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
     // this launch's activation rows into LDS
     if (!kQuant || c.dtype == MAMBO_DTYPE_MXFP8) {
-        // rows as 16-byte chunks (K is a multiple of 256, so none straddles rows), their
-        // scales as dwords (the host requires 4-byte aligned scale rows)
+        // rows as 16-byte chunks (K is a multiple of 256, so none straddles rows; slot e of
+        // row r takes chunk act_slot(e, r)), their scales as dwords (the host requires
+        // 4-byte aligned scale rows)
         const int nx = rows * K / 16;
         const __amdgpu_buffer_rsrc_t xr = byte_rsrc(c.x);
         for (int i = wave; 64 * i < nx; i += W) {
             const int e = 64 * i + lane, r = e * 16 / K;
             if (e < nx)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(smem + Ld.x + 1024 * i), 16,
-                                                         (uint32_t)(r * c.ldx + (e * 16 - r * K)), 0, 0, 0);
+                                                         (uint32_t)(r * c.ldx + 16 * act_slot(e - r * (K / 16), r)),
+                                                         0, 0, 0);
         }
         const int ns = rows * (K / 128);
         const __amdgpu_buffer_rsrc_t sr = byte_rsrc(c.xs);
@@ -281,7 +283,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
                 load_group32_coherent<false>(xr, (uint32_t)(4 * (r * c.ldx + 32 * gg)), v);
             uint32_t codes[8];
             const int scale = quantize_group32(v, codes);
-            uint4 *dst = reinterpret_cast<uint4 *>(smem + Ld.x + r * K + 32 * gg);
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + Ld.x + r * K + 16 * act_slot(2 * gg, r));
             dst[0] = uint4{codes[0], codes[1], codes[2], codes[3]};
             dst[1] = uint4{codes[4], codes[5], codes[6], codes[7]};
             smem[Ld.xs + r * gpr + gg] = (uint8_t)scale;
@@ -293,15 +295,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
     // block-diagonal operand of the rows (see gemm_stream_kernel)
     ALane al[1];
     {
-        const bool a_lane = (col >> 2) == q;
-        const int g_row = col >> 2;
-        const bool s_lane = ((lane >> 4) & 1) == (g_row >> 1);
         const int r = lane & 3;
-        const bool on = a_lane && r < rows, son = s_lane && r < rows;
-        al[0].x = on ? smem + Ld.x + r * K + 64 * q : smem + Ld.zero;
-        al[0].s = son ? smem + Ld.xs + r * (K / 32) + 2 * g_row : smem + Ld.zero + 64;
-        al[0].xstep = on ? 256 : 0;
-        al[0].sstep = son ? 8 : 0;
+        al[0] = a_lane<true>(lane, r < rows, smem + Ld.x + r * K, smem + Ld.xs + r * (K / 32), smem + Ld.zero,
+                       smem + Ld.zero + 64);
     }
     float acc[1][4] = {{0.0f, 0.0f, 0.0f, 0.0f}};
     float *red = reinterpret_cast<float *>(smem + Ld.red);
@@ -318,7 +314,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
             if (s < total) {
                 const int blk = wave + ci * W;
                 ATile<1> at;
-                load_a<1>(at, al, min(blk, B - 1));
+                load_a<1>(at, al, min(blk, B - 1), smem + Ld.zero);
+                __builtin_amdgcn_sched_barrier(0); // activation reads before the codebook reads
                 compute_block<1, kLg>(wr[jj], at, lut, c4, acc, blk < B);
                 if (++ci == steps) {
                     stream_tile_end<1, W, true>(acc, red + (tile_no & 1) * (W * 64), wave, tid, lane,

@@ -10,21 +10,22 @@
 // waves split the blocks of one K range and reduce through LDS; several workgroups may
 // split K further (f32 atomics into a zeroed output).
 //
-// Per super-block each lane decodes 16 four-weight codes (groups 2q and 2q+1 of row
-// col, q = lane/16, col = lane%16) straight into the B operand of
-// V_MFMA_SCALE_F32_16X16X128_F8F6F4: lane l of B holds 32 bytes of column col (K chunk
-// q: k in [16q, 16q+16) and [64+16q, 64+16q+16), byte t of lane l of A pairing with
-// byte t of lane l' of B for l >> 4 == l' >> 4), so one lane's decoded group is exactly
-// its B slice; nothing decoded touches HBM. Layout measured on gfx950 with one-hot
-// operands.
+// Per super-block each lane decodes 16 four-weight codes of row col (q = lane/16, col =
+// lane%16) straight into the B operand of V_MFMA_SCALE_F32_16X16X128_F8F6F4: lane l of
+// B holds 32 bytes of column col (K [16q, 16q+16) and [64+16q, 64+16q+16), byte t of
+// lane l of A pairing with byte t of lane l' of B for l >> 4 == l' >> 4), and the tile
+// layout (mambo_common.h) stores each lane's codes in exactly that order, so the decoded
+// words are its B slice as they are; nothing decoded touches HBM. Layout measured on
+// gfx950 with one-hot operands.
 //   code address: 2 VALU (funnel shift + mask of the 9-bit index stream)
 //   magnitude:    1 LDS read of the E4M3-encoded grid word
 //   signs:        2 VALU (rotate the bit-transposed sign word, bit-field insert)
-// Because F differs per 32-weight group and a K=128 MFMA spans four groups, the A
-// operand (activations) is block-diagonal: row i = 4*g' + m' of A holds activation row
-// m' only in K chunk g' (zero elsewhere). Output row (g', m') of lane l then carries the
-// partial dot product of exactly the group lane l decoded, so each lane post-scales its
-// own accumulator by its own group's F; the four g' partials are summed at the end.
+// Because F differs per 32-weight group and a K=128 MFMA spans four groups (one per K
+// block of 32), the A operand (activations) is block-diagonal: row i = 4*g + m' of A
+// holds activation row m' only in one K block (zero elsewhere), the block whose groups
+// make up scale byte g (out_block). Output row (g, m'), held by lane group g, then sums
+// exactly one group of its column, and each lane post-scales its own accumulator by the
+// F of the scale byte it loaded itself; the four K blocks' partials are summed at the end.
 // M up to 4 per MFMA, up to 16 per pass (U = 1..4 MFMAs per K step).
 #include <mutex>
 
@@ -96,15 +97,17 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         if constexpr (kLdsAct && kQ == 0) {
             // activation rows m0 .. m0+rows-1 as 16-byte chunks (K is a multiple of 256, so
-            // none straddles rows), then their scales as dwords (K/32 is a multiple of 8;
-            // the host stages only 4-byte aligned scale rows)
+            // none straddles rows; slot c of row r takes chunk act_slot(c, r)), then their
+            // scales as dwords (K/32 is a multiple of 8; the host stages only 4-byte aligned
+            // scale rows)
             const int nx = rows * K / 16;
             const __amdgpu_buffer_rsrc_t xr = byte_rsrc(xv + m0 * ldxv);
             for (int i = wave; 64 * i < nx; i += W) {
                 const int c = 64 * i + lane, r = c * 16 / K;
                 if (c < nx)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(smem + L.x + 1024 * i), 16,
-                                                             (uint32_t)(r * ldxv + (c * 16 - r * K)), 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        xr, (lds_ptr)(smem + L.x + 1024 * i), 16,
+                        (uint32_t)(r * ldxv + 16 * act_slot(c - r * (K / 16), r)), 0, 0, 0);
             }
             const int ns = rows * (K / 128);
             const __amdgpu_buffer_rsrc_t sr = byte_rsrc(xs + m0 * ldxs);
@@ -138,7 +141,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
                 load_group32<kQ == 1>(xv, (m0 + r) * ldxv + 32 * g, qv);
             uint32_t codes[8];
             const int scale = quantize_group32(qv, codes);
-            uint4 *dst = reinterpret_cast<uint4 *>(smem + L.x + r * K + 32 * g);
+            uint4 *dst = reinterpret_cast<uint4 *>(smem + L.x + r * K + 16 * act_slot(2 * g, r));
             dst[0] = uint4{codes[0], codes[1], codes[2], codes[3]};
             dst[1] = uint4{codes[4], codes[5], codes[6], codes[7]};
             smem[L.xs + r * (K / 32) + g] = (uint8_t)scale;
@@ -151,24 +154,21 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
     __builtin_amdgcn_s_waitcnt((kWLoads * (kDepth - 1)) | (7 << 4) | (15 << 8));
     __syncthreads();
 
-    const bool a_lane = (col >> 2) == q;
-    const int g_row = col >> 2;
-    const bool s_lane = ((lane >> 4) & 1) == (g_row >> 1);
+    const uint8_t *azero;
+    if constexpr (kLdsAct)
+        azero = smem + L.zero;
+    else
+        azero = g_zero_chunk;
     ALane al[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int r = 4 * u + (lane & 3); // row within the chunk
-        const bool on = a_lane && r < rows;
-        const bool son = s_lane && r < rows;
-        if constexpr (kLdsAct) {
-            al[u].x = on ? smem + L.x + r * K + 64 * q : smem + L.zero;
-            al[u].s = son ? smem + L.xs + r * (K / 32) + 2 * g_row : smem + L.zero + 64;
-        } else {
-            al[u].x = on ? xv + (m0 + r) * ldxv + 64 * q : g_zero_chunk;
-            al[u].s = son ? xs + (m0 + r) * ldxs + 2 * g_row : g_unit_scales;
-        }
-        al[u].xstep = on ? 256 : 0;
-        al[u].sstep = son ? 8 : 0;
+        if constexpr (kLdsAct)
+            al[u] = a_lane<true>(lane, r < rows, smem + L.x + r * K, smem + L.xs + r * (K / 32), smem + L.zero,
+                                 smem + L.zero + 64);
+        else
+            al[u] = a_lane<false>(lane, r < rows, xv + (m0 + r) * ldxv, xs + (m0 + r) * ldxs, g_zero_chunk,
+                                  g_unit_scales);
     }
 
     float acc[U][4];
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
         int as = 0, ai = 0; // the prefetch cursor's (s, i) for these first steps
 #pragma unroll
         for (int j = 0; j < kDepth - 1; ++j) {
-            load_a<U>(ar[j], al, min(first + ai * W, b_end - 1));
+            load_a<U, kLdsAct>(ar[j], al, min(first + ai * W, b_end - 1), azero);
             if (as + 1 < total) {
                 ++as;
                 if (++ai == steps)
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
             const int bp = min(first + pc.i * W, b_end - 1);
             wr[slot] = load_w_rsrc(pc.w, (uint32_t)bp * kTileBytes, lane, col);
             if constexpr (!kLdsAct)
-                load_a<U>(ar[slot], al, bp);
+                load_a<U, kLdsAct>(ar[slot], al, bp, azero);
             advance(pc, total, steps, ga, B);
             // keep the prefetch issued before the decode of step s (scheduler fence)
             if constexpr (MAMBO_SCHED_FENCE)
@@ -213,7 +213,12 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
             if (s < total) {
                 const int blk = first + ci * W;
                 if constexpr (kLdsAct) {
-                    load_a<U>(ar[0], al, min(blk, b_end - 1));
+                    // the activation reads go out before the codebook reads: LDS reads
+                    // complete in order, so the decode's partial waits then never wait
+                    // for them (left to the scheduler, they sank behind the codebook
+                    // reads at 2-4 tokens: 4% slower)
+                    load_a<U, kLdsAct>(ar[0], al, min(blk, b_end - 1), azero);
+                    __builtin_amdgcn_sched_barrier(0);
                     compute_block<U, kLg>(wr[j], ar[0], lut, c4, acc, blk < b_end);
                 } else {
                     compute_block<U, kLg>(wr[j], ar[j], lut, c4, acc, blk < b_end);
@@ -242,13 +247,13 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
 // Decode per code: the grid word in level form (bytes 0..7) from LDS selects, with one
 // v_perm_b32 each, the hi and lo bytes of four weights from the group's 16-byte split
 // table entry; the four signs are OR-ed into hi and XOR-ed into lo (lo has a sign).
-// The decoded group of lane (col, q) is its own group 2q+h; v_permlane16_swap then
-// exchanges half groups between lane groups 0<->1 and 2<->3, so that in MFMA h the K
-// blocks hold weight groups (kb0, kb1, kb2, kb3) = (h, 4+h, 2+h, 6+h) with both 16-byte
-// halves of a group inside one K block (one E8M0 activation scale per K block). The A
-// operand of lane (token i, q) takes the matching bytes: group 4*(q>>1) + h, half q&1,
-// and +64 bytes for group 4*(q>>1) + 2 + h. Scale lane i + 16*kb holds token i's scale
-// of group h + 4*(kb&1) + 2*(kb>>1).
+// The tile layout puts each lane's codes in the MFMA's K order (mambo_common.h): in MFMA
+// h the K blocks hold weight groups (kb0, kb1, kb2, kb3) = (h, 4+h, 2+h, 6+h), each group
+// inside one K block (one E8M0 activation scale per K block), and lane (col, q) decodes
+// half q&1 of groups 4*(q>>1) + h (bytes 0-15) and 4*(q>>1) + 2 + h (bytes 16-31): the
+// decoded words are its operand as they are. The A operand of lane (token i, q) takes
+// the matching bytes: group 4*(q>>1) + h, half q&1, and +64 bytes for group 4*(q>>1) +
+// 2 + h. Scale lane i + 16*kb holds token i's scale of group h + 4*(kb&1) + 2*(kb>>1).
 
 struct ADense {
     v8i a[2];
@@ -297,53 +302,55 @@ __device__ __forceinline__ void split_word(uint32_t lv, uint32_t p, uint4 tab, i
     lo = (int)__builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(tab.w, tab.z, lv), r, 0x80808080u, 0x78);
 }
 
+// Split-table entry of operand half X (0: bytes 0-15, 1: bytes 16-31) of MFMA H, from the
+// lane's dense scale word (dense_scales: nibble 2X + H).
+template <int H, int X>
+__device__ __forceinline__ uint4 split_entry(const uint4 *split, uint32_t sc)
+{
+    return split[(sc >> (4 * (2 * X + H))) & 15u];
+}
+
+// MFMA H's hi and lo operands: codes 0-3 with the entry of half 0 (ta), 4-7 of half 1 (tb).
 template <int H, int... C>
-__device__ __forceinline__ void decode_split(const uint32_t (&s)[5], uint32_t p, const uint8_t *lvl, uint4 tab,
-                                             v8i &bhi, v8i &blo, std::integer_sequence<int, C...>)
+__device__ __forceinline__ void decode_split(const uint32_t (&s)[5], uint32_t p, const uint8_t *lvl, uint4 ta,
+                                             uint4 tb, v8i &bhi, v8i &blo, std::integer_sequence<int, C...>)
 {
     int h[8], l[8];
-    (split_word<C>(*reinterpret_cast<const uint32_t *>(lvl + code_addr<8 * H + C>(s)), p, tab, h[C], l[C]), ...);
+    (split_word<C>(*reinterpret_cast<const uint32_t *>(lvl + code_addr<8 * H + C>(s)), p, C < 4 ? ta : tb, h[C],
+                   l[C]),
+     ...);
     bhi = v8i{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
     blo = v8i{l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
 }
 
-// Own-group order (bytes 0-15 / 16-31 = first / second half of the lane's group) to the
-// dense MFMA K order: lane group 1's first half <-> lane group 0's second half (and 3/2).
-__device__ __forceinline__ void to_dense_order(v8i &b)
+// Both halves of one tile-block (MFMA H = 0, 1).
+__device__ __forceinline__ void decode_block(const WTile &w, const uint8_t *lvl, const uint4 *split, v8i (&bh)[2],
+                                             v8i (&bl)[2])
 {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)b[k], (uint32_t)b[4 + k], false, false);
-        b[k] = (int)r[0];
-        b[4 + k] = (int)r[1];
-    }
+    const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
+    const uint32_t sc = dense_scales(w.sc);
+    decode_split<0>(s, w.sg.x, lvl, split_entry<0, 0>(split, sc), split_entry<0, 1>(split, sc), bh[0], bl[0],
+                    std::make_integer_sequence<int, 8>{});
+    decode_split<1>(s, w.sg.y, lvl, split_entry<1, 0>(split, sc), split_entry<1, 1>(split, sc), bh[1], bl[1],
+                    std::make_integer_sequence<int, 8>{});
 }
 
 template <int MC>
 __device__ __forceinline__ void compute_dense(const WTile &w, const ADense (&at)[MC], const uint8_t *lvl,
                                               const uint4 *split, float (&acc)[MC][4], bool valid)
 {
-    const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
-    const uint32_t sc = w.sc;
-    const uint4 t0 = split[sc & 15u];
-    const uint4 t1 = split[sc >> 4];
-    v8i h0, l0, h1, l1;
-    decode_split<0>(s, w.sg.x, lvl, t0, h0, l0, std::make_integer_sequence<int, 8>{});
-    decode_split<1>(s, w.sg.y, lvl, t1, h1, l1, std::make_integer_sequence<int, 8>{});
-    to_dense_order(h0);
-    to_dense_order(l0);
-    to_dense_order(h1);
-    to_dense_order(l1);
+    v8i bh[2], bl[2];
+    decode_block(w, lvl, split, bh, bl);
     // B scale 2^1: the split terms are stored halved. Per 16-token chunk one chain of four
     // MFMAs on the one decode (the callers interleave the chains of their NT tiles).
     const float f = valid ? half_bits_to_float((uint16_t)w.dh) : 0.0f;
 #pragma unroll
     for (int u = 0; u < MC; ++u) {
         const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-        v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[0], h0, zero, 0, 0, 0, (int)at[u].s[0], 0, 128);
-        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[0], l0, c, 0, 0, 0, (int)at[u].s[0], 0, 128);
-        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[1], h1, c, 0, 0, 0, (int)at[u].s[1], 0, 128);
-        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[1], l1, c, 0, 0, 0, (int)at[u].s[1], 0, 128);
+        v4f c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[0], bh[0], zero, 0, 0, 0, (int)at[u].s[0], 0, 128);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[0], bl[0], c, 0, 0, 0, (int)at[u].s[0], 0, 128);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[1], bh[1], c, 0, 0, 0, (int)at[u].s[1], 0, 128);
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at[u].a[1], bl[1], c, 0, 0, 0, (int)at[u].s[1], 0, 128);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             acc[u][r] = __builtin_fmaf(c[r], f, acc[u][r]);
@@ -675,14 +682,7 @@ __device__ __forceinline__ void decode_tiles(const WTile (&w)[NT], const uint8_t
 {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t s5[5] = {w[nt].ia.x, w[nt].ia.y, w[nt].ia.z, w[nt].ia.w, (uint32_t)w[nt].ib};
-        const uint4 t0 = split[w[nt].sc & 15u], t1 = split[(uint32_t)w[nt].sc >> 4];
-        decode_split<0>(s5, w[nt].sg.x, lvl, t0, bh[nt][0], bl[nt][0], std::make_integer_sequence<int, 8>{});
-        decode_split<1>(s5, w[nt].sg.y, lvl, t1, bh[nt][1], bl[nt][1], std::make_integer_sequence<int, 8>{});
-        to_dense_order(bh[nt][0]);
-        to_dense_order(bl[nt][0]);
-        to_dense_order(bh[nt][1]);
-        to_dense_order(bl[nt][1]);
+        decode_block(w[nt], lvl, split, bh[nt], bl[nt]);
         d[nt] = half_bits_to_float((uint16_t)w[nt].dh);
     }
 }
@@ -737,11 +737,9 @@ __device__ __forceinline__ void decode_half(const WTile (&w)[NT], const uint8_t 
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const uint32_t s5[5] = {w[nt].ia.x, w[nt].ia.y, w[nt].ia.z, w[nt].ia.w, (uint32_t)w[nt].ib};
-        const uint4 t = split[H == 0 ? (w[nt].sc & 15u) : ((uint32_t)w[nt].sc >> 4)];
-        decode_split<H>(s5, H == 0 ? w[nt].sg.x : w[nt].sg.y, lvl, t, bh[nt], bl[nt],
-                        std::make_integer_sequence<int, 8>{});
-        to_dense_order(bh[nt]);
-        to_dense_order(bl[nt]);
+        const uint32_t sc = dense_scales(w[nt].sc);
+        decode_split<H>(s5, H == 0 ? w[nt].sg.x : w[nt].sg.y, lvl, split_entry<H, 0>(split, sc),
+                        split_entry<H, 1>(split, sc), bh[nt], bl[nt], std::make_integer_sequence<int, 8>{});
     }
 }
 
@@ -942,17 +940,22 @@ __global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__res
     }
 
     // D[i][j] of sub-tile (mt, nt): lane j + 16*(i/4), register i%4 -> token
-    // m0 + 16*mt + 4q + r, weight row 16*tile + col.
+    // m0 + 16*mt + 4q + r, weight row 16*tile + col. The lane's col and q are recomputed
+    // here from the lane count (v_mbcnt) rather than kept from the thread id across the
+    // block loop: in the 256 x 256 x 16 tile (128 VGPRs) keeping them spilled two
+    // registers, and a kernel with spills takes scratch memory at every dispatch.
+    const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int col_e = lane_e & 15, q_e = lane_e >> 4;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const int64_t n = tile[nt] * kTileRows + col;
+        const int64_t n = tile[nt] * kTileRows + col_e;
         if (n >= N)
             continue;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + 16 * mt + 4 * q + r;
+                const int64_t m = m0 + 16 * mt + 4 * q_e + r;
                 if (m < M) {
                     if (atomic)
                         atomicAdd(out + m * ldo + n, acc[mt][nt][r]);
@@ -994,15 +997,19 @@ struct Decoded {
     float d;
 };
 
-// Per-code pieces of the decode (decode_split split into steps).
+// Per-code pieces of the decode (decode_split split into steps). Code I (0..15) is code
+// I % 8 of MFMA I / 8; codes 4k .. 4k+3 use split-table entry k, which the fetch of code
+// 4k reads into slot k & 1 (the finish of code 4k-1, one step behind, still reads the
+// other slot), so only two entries are held.
 struct DecodeState {
     uint32_t s[5];   // index bit stream
-    uint32_t p[2];   // transposed sign words of the lane's two groups
-    uint4 tab[2];    // split-table entries of the two groups' scale nibbles
+    uint32_t p[2];   // transposed sign words of the lane's two halves
+    uint32_t sc;     // scale nibbles (dense_scales)
+    uint4 tab[2];    // split-table entries in use
     float d;         // the row's d in f32
 };
 
-__device__ __forceinline__ void decode_begin(DecodeState &st, const WTile &w, const uint4 *split)
+__device__ __forceinline__ void decode_begin(DecodeState &st, const WTile &w)
 {
     st.s[0] = w.ia.x;
     st.s[1] = w.ia.y;
@@ -1011,8 +1018,7 @@ __device__ __forceinline__ void decode_begin(DecodeState &st, const WTile &w, co
     st.s[4] = (uint32_t)w.ib;
     st.p[0] = w.sg.x;
     st.p[1] = w.sg.y;
-    st.tab[0] = split[w.sc & 15u];
-    st.tab[1] = split[(uint32_t)w.sc >> 4];
+    st.sc = dense_scales(w.sc);
     // d becomes an f32 register here, where the decode waits for this block's weights
     // anyway. Left as the raw fp16 word, the compiler folded the conversion into the
     // post-scale (v_fma_mix) and carried the word of the block two ahead across the loop
@@ -1023,8 +1029,10 @@ __device__ __forceinline__ void decode_begin(DecodeState &st, const WTile &w, co
 }
 
 template <int I>
-__device__ __forceinline__ uint32_t decode_fetch(const DecodeState &st, const uint8_t *lvl)
+__device__ __forceinline__ uint32_t decode_fetch(DecodeState &st, const uint8_t *lvl, const uint4 *split)
 {
+    if constexpr (I % 4 == 0)
+        st.tab[(I / 4) & 1] = split_entry<I / 8, (I / 4) & 1>(split, st.sc);
     return *reinterpret_cast<const uint32_t *>(lvl + code_addr<I>(st.s));
 }
 
@@ -1033,13 +1041,9 @@ __device__ __forceinline__ void decode_finish(const DecodeState &st, uint32_t lv
 {
     constexpr int H = I / 8, C = I % 8;
     int hi, lo;
-    split_word<C>(lv, st.p[H], st.tab[H], hi, lo);
+    split_word<C>(lv, st.p[H], st.tab[(I / 4) & 1], hi, lo);
     out.hi[H][C] = hi;
     out.lo[H][C] = lo;
-    if constexpr (C == 7) {
-        to_dense_order(out.hi[H]);
-        to_dense_order(out.lo[H]);
-    }
 }
 
 // Copies of block b's activations into one buffer of the prefill LDS (values `vals`, scales
@@ -1090,9 +1094,10 @@ __device__ __forceinline__ void prefill_load(PrefillPipe &pp, int slot, const ui
 // `cur`, the next sub-tile's loads, code mt of the next block's decode requested and code
 // mt-1 finished into `nxt`, sub-tile mt-1 scaled into its accumulators.
 template <int mt>
-__device__ __forceinline__ void prefill_step(PrefillPipe &pp, const Decoded &cur, Decoded &nxt, const DecodeState &st,
+__device__ __forceinline__ void prefill_step(PrefillPipe &pp, const Decoded &cur, Decoded &nxt, DecodeState &st,
                                              const uint8_t *vals, const uint8_t *scl, const uint32_t (&ao)[2][2],
-                                             uint32_t soff, const uint8_t *lvl, float d, float (&acc)[16][4])
+                                             uint32_t soff, const uint8_t *lvl, const uint4 *split, float d,
+                                             float (&acc)[16][4])
 {
     constexpr int sl = mt % (kPrefillAhead + 1), cw = mt & 1;
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1103,7 +1108,7 @@ __device__ __forceinline__ void prefill_step(PrefillPipe &pp, const Decoded &cur
     if constexpr (mt + kPrefillAhead < 16)
         prefill_load(pp, (mt + kPrefillAhead) % (kPrefillAhead + 1), vals + 4096 * (mt + kPrefillAhead), ao,
                      scl + 128 * (mt + kPrefillAhead) + soff);
-    pp.lw[cw] = decode_fetch<mt>(st, lvl);
+    pp.lw[cw] = decode_fetch<mt>(st, lvl, split);
     if constexpr (mt > 0) {
         decode_finish<mt - 1>(st, pp.lw[cw ^ 1], nxt);
 #pragma unroll
@@ -1115,19 +1120,19 @@ __device__ __forceinline__ void prefill_step(PrefillPipe &pp, const Decoded &cur
 }
 
 template <int... MT>
-__device__ __forceinline__ void prefill_steps(PrefillPipe &pp, const Decoded &cur, Decoded &nxt, const DecodeState &st,
+__device__ __forceinline__ void prefill_steps(PrefillPipe &pp, const Decoded &cur, Decoded &nxt, DecodeState &st,
                                               const uint8_t *vals, const uint8_t *scl, const uint32_t (&ao)[2][2],
-                                              uint32_t soff, const uint8_t *lvl, float d, float (&acc)[16][4],
-                                              std::integer_sequence<int, MT...>)
+                                              uint32_t soff, const uint8_t *lvl, const uint4 *split, float d,
+                                              float (&acc)[16][4], std::integer_sequence<int, MT...>)
 {
-    (prefill_step<MT>(pp, cur, nxt, st, vals, scl, ao, soff, lvl, d, acc), ...);
+    (prefill_step<MT>(pp, cur, nxt, st, vals, scl, ao, soff, lvl, split, d, acc), ...);
 }
 
 template <int... I>
-__device__ __forceinline__ void decode_all(const DecodeState &st, const uint8_t *lvl, Decoded &out,
+__device__ __forceinline__ void decode_all(DecodeState &st, const uint8_t *lvl, const uint4 *split, Decoded &out,
                                            std::integer_sequence<int, I...>)
 {
-    ((decode_finish<I>(st, decode_fetch<I>(st, lvl), out)), ...);
+    ((decode_finish<I>(st, decode_fetch<I>(st, lvl, split), out)), ...);
 }
 
 template <int W>
@@ -1184,7 +1189,15 @@ __global__ __launch_bounds__(W * 64) void gemm_prefill_kernel(const uint8_t *__r
         const int row = 4 * (wave + W * j) + (lane >> 4);
         voff[j] = (uint32_t)min(row, last_row) * (uint32_t)ldxv + 16u * (uint32_t)((lane & 15) ^ (row & 15));
     }
-    const uint32_t soff_stage = (uint32_t)min(32 * wave + (lane >> 1), last_row) * (uint32_t)ldxs + 4u * (lane & 1);
+    // Offset of this lane's scale copy: recomputed per block from a lane id the compiler
+    // cannot see through (three VALU instructions). Hoisted out of the loop it was the
+    // register spilled at 256 VGPRs, and its reload (a scratch load, counted with the
+    // weight loads) made every block wait for all loads in flight before its copies.
+    auto stage_soff = [&]() {
+        uint32_t l = (uint32_t)lane;
+        asm volatile("" : "+v"(l));
+        return (uint32_t)min(32 * wave + (int)(l >> 1), last_row) * (uint32_t)ldxs + 4u * (l & 1);
+    };
 
     // A operand of lane (token row col of a sub-tile, q), K half h: 16-byte chunks
     // 8*(q>>1) + (q&1) + 2h and +4 of the row at their swizzled slots (the dense kernel's
@@ -1216,11 +1229,11 @@ __global__ __launch_bounds__(W * 64) void gemm_prefill_kernel(const uint8_t *__r
     {
         const WTile w0 = load_w_rsrc<0>(wt, wblock(b0), lane, col);
         wslot[0] = load_w_rsrc<0>(wt, wblock(b0 + 1), lane, col);
-        prefill_stage<W>(s_vals0, s_scale0, b0, xrows, srows, voff, soff_stage, wave);
+        prefill_stage<W>(s_vals0, s_scale0, b0, xrows, srows, voff, stage_soff(), wave);
         __syncthreads(); // codebook and split tables
         DecodeState st;
-        decode_begin(st, w0, s_split);
-        decode_all(st, lvl, dec[0], std::make_integer_sequence<int, 16>{});
+        decode_begin(st, w0);
+        decode_all(st, lvl, s_split, dec[0], std::make_integer_sequence<int, 16>{});
         dec[0].d = st.d;
     }
     __syncthreads();
@@ -1233,14 +1246,14 @@ __global__ __launch_bounds__(W * 64) void gemm_prefill_kernel(const uint8_t *__r
         const uint8_t *vals_ = (C) ? s_vals1 : s_vals0;                                                            \
         const uint8_t *scl_ = (C) ? s_scale1 : s_scale0;                                                           \
         prefill_stage<W>((C) ? s_vals0 : s_vals1, (C) ? s_scale0 : s_scale1, min(b + 1, b1 - 1), xrows, srows,     \
-                         voff, soff_stage, wave);                                                                  \
+                         voff, stage_soff(), wave);                                                                \
         wslot[(C) ^ 1] = load_w_rsrc<0>(wt, wblock(b + 2), lane, col);                                             \
         DecodeState st_;                                                                                           \
-        decode_begin(st_, wslot[C], s_split);                                                                      \
+        decode_begin(st_, wslot[C]);                                                                               \
         PrefillPipe pp_;                                                                                           \
         for (int t_ = 0; t_ < kPrefillAhead; ++t_)                                                                 \
             prefill_load(pp_, t_, vals_ + 4096 * t_, ao, scl_ + 128 * t_ + soff);                                  \
-        prefill_steps(pp_, dec[C], dec[(C) ^ 1], st_, vals_, scl_, ao, soff, lvl, dec[C].d, acc,                   \
+        prefill_steps(pp_, dec[C], dec[(C) ^ 1], st_, vals_, scl_, ao, soff, lvl, s_split, dec[C].d, acc,          \
                       std::make_integer_sequence<int, 16>{});                                                      \
         decode_finish<15>(st_, pp_.lw[1], dec[(C) ^ 1]);                                                           \
         dec[(C) ^ 1].d = st_.d;                                                                                    \

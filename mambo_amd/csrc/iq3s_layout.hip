@@ -87,15 +87,27 @@ __device__ __forceinline__ uint32_t le32(const uint8_t *p)
     return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
-// Bit (c + 8j) of the result = bit (4c + j) of the group's sign word.
-__device__ __forceinline__ uint32_t transpose_signs(uint32_t s)
+// Code c (0..63: weights 4c..4c+3 of the block) of slot i (0..15) of lane group q (tile
+// layout in mambo_common.h).
+__device__ __forceinline__ int slot_code(int q, int i)
+{
+    const int h = i >> 3, c = i & 7;
+    return 8 * tile_group(2 * (c >> 2) + (q >> 1), h) + 4 * (q & 1) + (c & 3);
+}
+
+// Transposed sign word of half h of lane group q: bit (C + 8j) = sign of weight j of slot
+// 8h + C, i.e. bit 4*code + j of the block's sign bits (bytes 74..105, weight k at bit k).
+__device__ __forceinline__ uint32_t half_signs(const uint8_t *o, int q, int h)
 {
     uint32_t p = 0;
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < 8; ++c) {
+        const int code = slot_code(q, 8 * h + c);
+        const uint32_t nib = ((uint32_t)o[74 + code / 2] >> (4 * (code & 1))) & 15u;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            p |= ((s >> (4 * c + j)) & 1u) << (c + 8 * j);
+            p |= ((nib >> j) & 1u) << (c + 8 * j);
+    }
     return p;
 }
 
@@ -109,7 +121,7 @@ __device__ void write_tile(uint8_t (*blk)[112], uint8_t *__restrict__ tile)
         uint32_t w[5] = {0, 0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int c = 16 * q + i; // code index within the block
+            const int c = slot_code(q, i);
             const uint32_t idx = o[2 + c] | ((((uint32_t)o[66 + c / 8] >> (c % 8)) & 1u) << 8);
             const int p = 9 * i;
             w[p >> 5] |= idx << (p & 31);
@@ -118,9 +130,7 @@ __device__ void write_tile(uint8_t (*blk)[112], uint8_t *__restrict__ tile)
         }
         *reinterpret_cast<uint4 *>(tile + kTileIdxA + 16 * l) = make_uint4(w[0], w[1], w[2], w[3]);
         *reinterpret_cast<uint16_t *>(tile + kTileIdxB + 2 * l) = (uint16_t)w[4];
-        const uint32_t s0 = transpose_signs(le32(o + 74 + 4 * (2 * q)));
-        const uint32_t s1 = transpose_signs(le32(o + 74 + 4 * (2 * q + 1)));
-        *reinterpret_cast<uint2 *>(tile + kTileSigns + 8 * l) = make_uint2(s0, s1);
+        *reinterpret_cast<uint2 *>(tile + kTileSigns + 8 * l) = make_uint2(half_signs(o, q, 0), half_signs(o, q, 1));
         tile[kTileScales + l] = o[106 + q];
         if (q == 0) {
             tile[kTileD + 2 * r] = o[0];

@@ -18,7 +18,7 @@ __constant__ GridTables c_grid = kGridTables;
 // Kept in the global address space (not constant) so the activation pointers stay
 // global and the loads are global_load, not flat_load.
 __device__ __align__(16) uint8_t g_zero_chunk[64] = {};
-__device__ uint8_t g_unit_scales[2] = {127, 127};
+__device__ __align__(4) uint8_t g_unit_scales[2] = {127, 127};
 __constant__ SplitTables c_split = kSplitTables;
 
 // The stream kernel's codebook in LDS holds 2^kLg copies of every E4M3 grid word: word
@@ -78,8 +78,8 @@ constexpr int kDepth = MAMBO_STREAM_DEPTH;
 struct WTile {
     uint4 ia;     // idx stream bits 0..127
     uint16_t ib;  // idx stream bits 128..143
-    uint2 sg;     // transposed sign words, groups 2q and 2q+1
-    uint8_t sc;   // scale nibbles of groups 2q, 2q+1
+    uint2 sg;     // transposed sign words of the halves h = 0, 1
+    uint8_t sc;   // scale byte q of row col: nibbles of groups 2q, 2q+1
     uint16_t dh;  // fp16 d of row col
 };
 
@@ -98,7 +98,7 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 
 // One lane's share of a tile-block (load_w_rsrc): the block at byte `step` past the
 // resource base, in kWLoads vector memory instructions (codes b128 + b16, signs b64,
-// scale nibbles b8, the row's fp16 d b16).
+// scale nibbles b8 or b16, the row's fp16 d b16).
 constexpr int kWLoads = 5;
 // Cache policy of the decode kernels' weight loads: non-temporal (gfx940-family CPol NT
 // bit). Each weight byte is read once per launch; marking the stream for early eviction
@@ -107,6 +107,7 @@ constexpr int kWLoads = 5;
 // tiled kernel re-reads each weight tile once per token tile and keeps the default
 // policy (NT measured 5% slower at M=2048).
 constexpr int kStreamPolicy = 2;
+
 template <int kPolicy = kStreamPolicy>
 __device__ __forceinline__ WTile load_w_rsrc(__amdgpu_buffer_rsrc_t r, uint32_t step, uint32_t lane, uint32_t col)
 {
@@ -120,6 +121,19 @@ __device__ __forceinline__ WTile load_w_rsrc(__amdgpu_buffer_rsrc_t r, uint32_t 
     w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, lane + kTileScales, step, kWeightPolicy);
     w.dh = __builtin_amdgcn_raw_buffer_load_b16(r, 2u * col + kTileD, step, kWeightPolicy);
     return w;
+}
+
+// The dense operands' scale nibbles from the lane's scale byte (WTile::sc: scales[q] of
+// its row, groups 2q and 2q+1): the 16 bits of groups 4qq .. 4qq+3 (qq = q >> 1), nibble
+// h = group tile_group(qq, h) (operand bytes 0-15 of half h), nibble 2 + h = group
+// tile_group(2 + qq, h) (bytes 16-31). Bytes 2qq and 2qq+1 are the scale bytes of lane
+// groups 2qq and 2qq+1, so one row swap brings in the partner's: after
+// v_permlane16_swap(x, x) the first result holds the even lane group's byte and the
+// second the odd one's, in both lanes of the pair. All 64 lanes must be active.
+__device__ __forceinline__ uint32_t dense_scales(uint32_t sc)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(sc, sc, false, false);
+    return r[0] | (r[1] << 8);
 }
 
 // Byte address (idx << 2) of code I's grid word; idx = bits [9I, 9I+9) of the stream.
@@ -203,7 +217,9 @@ __device__ __forceinline__ void sign_codes(const uint32_t (&mag)[16], uint32_t p
         sign_codes<I0 + 1, N - 1>(mag, p0, p1, b0, b1);
     }
 }
-template <int kLg, int kB, int K = 0>
+// Batches K .. KEnd-1 (of 16 / kB); a caller may stop after the batches of b0 (codes 0-7)
+// and continue later with the rest.
+template <int kLg, int kB, int K = 0, int KEnd = 16 / kB>
 __device__ __forceinline__ void decode_batched(const uint32_t (&s)[5], uint32_t p0, uint32_t p1, const uint8_t *lut,
                                                uint32_t c4, uint32_t (&mag)[16], v8i &b0, v8i &b1)
 {
@@ -216,44 +232,94 @@ __device__ __forceinline__ void decode_batched(const uint32_t (&s)[5], uint32_t 
     }
     __builtin_amdgcn_sched_barrier(0);
     sign_codes<K * kB, kB>(mag, p0, p1, b0, b1);
-    if constexpr ((K + 1) * kB < 16)
-        decode_batched<kLg, kB, K + 1>(s, p0, p1, lut, c4, mag, b0, b1);
+    if constexpr (K + 1 < KEnd)
+        decode_batched<kLg, kB, K + 1, KEnd>(s, p0, p1, lut, c4, mag, b0, b1);
 }
 
 template <int U>
 struct ATile {
     v8i a[U][2];
-    uint8_t s[U][2];
+    int s[U]; // E8M0 scales of the two K halves in bytes 0 and 1 (the MFMA picks byte h)
 };
 
-// Activation operand of one lane. Data: lane l holds row i = l & 15 = 4*g' + m' in K
-// chunk l >> 4 and is non-zero only when that chunk is g' (block-diagonal). Scales: the
-// E8M0 scale of (row i, K block kb) comes from lane i + 16*kb, and a lane's 32 bytes span
-// two K blocks (bytes 0-15 in block q/2, bytes 16-31 in block 2 + q/2), so the lanes
-// holding row i's scales are those with kb & 1 == g' >> 1. Lanes outside the diagonal
-// (and rows past M) point at a zero chunk / unit scales with a zero stride.
+// Activation operand of one lane. Data: row i = 4*g + m' of A holds activation row m'
+// only in K block kb = out_block(g) (block-diagonal), so output row i, which lane group g
+// holds, sums exactly weight group tile_group(kb, h) of its column: the groups of scale
+// byte g, the byte that lane group g loads (post-scale by its own F, no cross-lane
+// moves). Lane l holds row i = l & 15 at K [16q, 16q+16) (bytes 0-15, in K block q >> 1)
+// and [64+16q, 64+16q+16) (bytes 16-31, K block 2 + (q >> 1)), q = l >> 4: its 16
+// activation bytes sit in the low half when kb < 2, the high half otherwise, and only
+// when kb & 1 == q >> 1. Scales: the E8M0 scale of (row i, K block kb) comes from lane
+// i + 16*kb (see a_lane). Halves off the diagonal (and rows past M) point at a zero
+// chunk / unit scales with a zero stride.
 struct ALane {
-    const uint8_t *x;  // activation bytes of this lane's chunk, block 0
-    const uint8_t *s;  // E8M0 scale of this lane's chunk, block 0
-    int xstep;         // 256 or 0
-    int sstep;         // 8 or 0
+    const uint8_t *x;    // activation bytes of this lane's non-zero half (or zero), block 0
+    const uint8_t *s;    // E8M0 scale of this lane's K block, block 0
+    int xstep;           // 256 or 0
+    int sstep;           // 8 or 0
+    bool hi;             // the non-zero half is bytes 16-31
 };
 
-template <int U>
-__device__ __forceinline__ void load_a(ATile<U> &at, const ALane (&al)[U], int b)
+// zero: 64 zero bytes (the other half of every lane reads 16 of them). kAligned: the
+// scale rows are 2-byte aligned (the LDS copy), so both scale bytes come in one read.
+template <int U, bool kAligned = true>
+__device__ __forceinline__ void load_a(ATile<U> &at, const ALane (&al)[U], int b, const uint8_t *zero)
 {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint8_t *xp = al[u].x + b * al[u].xstep;
+        const uint8_t *xl = al[u].hi ? zero : xp;
+        const uint8_t *xh = al[u].hi ? xp : zero;
         const uint8_t *sp = al[u].s + b * al[u].sstep;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(xp + 32 * h);
-            const uint4 lo = p[0], hi = p[1];
+            const uint4 lo = *reinterpret_cast<const uint4 *>(xl + 32 * h);
+            const uint4 hi = *reinterpret_cast<const uint4 *>(xh + 32 * h);
             at.a[u][h] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-            at.s[u][h] = sp[h];
         }
+        // groups tile_group(kb, 0) and tile_group(kb, 1): adjacent bytes
+        if constexpr (kAligned)
+            at.s[u] = *reinterpret_cast<const uint16_t *>(sp);
+        else
+            at.s[u] = (int)sp[0] | ((int)sp[1] << 8);
     }
+}
+
+// K block whose weight groups tile_group(kb, 0..1) make up scale byte g: the bit swap
+// {0, 2, 1, 3}.
+__host__ __device__ constexpr int out_block(int g) { return ((g & 1) << 1) | (g >> 1); }
+
+// The stream kernels' LDS copy of the activation rows: 16-byte chunk c of row r lies at
+// chunk slot act_slot(c, r) of the row, a permutation inside each 256-byte block (c and
+// slot differ in bits 2-3 only), so that the four rows one operand read reaches at the
+// same K position fall in different banks instead of all in the same ones (rows lie K
+// bytes apart). An involution: the slot of a chunk and the chunk of a slot are the same.
+__host__ __device__ constexpr int act_slot(int c, int r) { return c ^ (4 * (r & 3)); }
+
+// Operand pointers of lane `lane` for the block-diagonal A above: token row r of the
+// chunk (r = 4u + (lane & 3)) has its activation bytes at `row` and its scales at `srow`;
+// `valid` is false when r is past M. `zero` = 64 zero bytes, `unit` = two unit scales.
+// kSwizzled: `row` is an LDS copy in the act_slot order. Selects only (no indexing by a
+// lane-dependent value), so everything stays in registers.
+template <bool kSwizzled>
+__device__ __forceinline__ ALane a_lane(int lane, bool valid, const uint8_t *row, const uint8_t *srow,
+                                        const uint8_t *zero, const uint8_t *unit)
+{
+    const int kb = out_block((lane & 15) >> 2), q = lane >> 4;
+    const bool on = valid && (kb & 1) == (q >> 1);
+    // chunk of K half 0; half 1 is 2 chunks on (bit 1, which act_slot leaves alone)
+    const int c0 = 2 * tile_group(kb, 0) + (q & 1);
+    ALane a;
+    a.x = on ? row + 16 * (kSwizzled ? act_slot(c0, lane & 3) : c0) : zero;
+    a.xstep = on ? 256 : 0;
+    a.hi = kb >= 2;
+    // Every lane of row i carries the row's own scale, also for the K blocks where the
+    // row is zero (0 x any scale adds nothing, and a non-finite scale reaches only the
+    // row's own output, as its own block already does). Only the four lanes q == kb
+    // reading it and the rest a shared unit scale measured 5% slower at 4 tokens.
+    a.s = valid ? srow + tile_group(kb, 0) : unit;
+    a.sstep = valid ? 8 : 0;
+    return a;
 }
 
 template <int U, int kLg>
@@ -262,26 +328,35 @@ __device__ __forceinline__ void compute_block(const WTile &w, const ATile<U> &at
 {
     const uint32_t s[5] = {w.ia.x, w.ia.y, w.ia.z, w.ia.w, (uint32_t)w.ib};
     const float d = half_bits_to_float((uint16_t)w.dh);
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
     v8i b0, b1;
+    v4f c0[U];
     if constexpr (kLg == 0) {
+        // half 0's MFMAs go out as soon as its codes are decoded, ahead of the waits for
+        // half 1's codebook reads (left to the scheduler, they waited for every read)
         uint32_t mag[16];
-        decode_batched<kLg, 4>(s, w.sg.x, w.sg.y, lut, c4, mag, b0, b1);
+        decode_batched<kLg, 4, 0, 2>(s, w.sg.x, w.sg.y, lut, c4, mag, b0, b1);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            c0[u] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][0], b0, zero, 0, 0, 0, at.s[u], 0, 127);
+        decode_batched<kLg, 4, 2>(s, w.sg.x, w.sg.y, lut, c4, mag, b0, b1);
     } else {
         b0 = decode_group<0, kLg>(s, w.sg.x, lut, c4, std::make_integer_sequence<int, 8>{});
         b1 = decode_group<1, kLg>(s, w.sg.y, lut, c4, std::make_integer_sequence<int, 8>{});
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            c0[u] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][0], b0, zero, 0, 0, 0, at.s[u], 0, 127);
     }
     const uint32_t sc = w.sc;
     // A block past the wave's range (a duplicate of its last block) contributes nothing.
     const float f0 = valid ? d * (float)(1u + 2u * (sc & 15u)) : 0.0f;
     const float f1 = valid ? d * (float)(1u + 2u * (sc >> 4)) : 0.0f;
-    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        v4f c0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][0], b0, zero, 0, 0, 0, (int)at.s[u][0], 0, 127);
-        v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][1], b1, zero, 0, 0, 0, (int)at.s[u][1], 0, 127);
+        v4f c1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(at.a[u][1], b1, zero, 0, 0, 1, at.s[u], 0, 127);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            acc[u][r] = __builtin_fmaf(c1[r], f1, __builtin_fmaf(c0[r], f0, acc[u][r]));
+            acc[u][r] = __builtin_fmaf(c1[r], f1, __builtin_fmaf(c0[u][r], f0, acc[u][r]));
     }
 }
 

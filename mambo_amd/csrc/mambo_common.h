@@ -38,17 +38,26 @@ constexpr int kIq3sBlockValues = 256;
 
 // Private tile layout written by mambo_iq3s_prepare/mambo_iq3s_pack and read by the
 // projection kernels. One tile = 16 weight rows x one super-block = 1760 bytes,
-// tiles ordered [row_tile][block]. Lane l of a 64-lane wave (col = l & 15 = row in the
-// tile, q = l >> 4) owns groups 2q and 2q+1 of its row:
+// tiles ordered [row_tile][block].
+//
+// The order is the B operand of V_MFMA_SCALE_F32_16X16X128_F8F6F4 over a block's two K
+// halves h: lane l (col = l & 15 = row in the tile, q = l >> 4) holds bytes 0-15 at K
+// [16q, 16q+16) and bytes 16-31 at K [64+16q, 64+16q+16) of column col, and K block kb
+// (K [32kb, 32kb+32), one E8M0 activation scale) of half h holds weight group
+// tile_group(kb, h) = {0, 4, 2, 6}[kb] + h. So in half h lane l decodes code slots
+// C = 0..7 (slot i = 8h + C of its stream): C < 4 are codes 4(q&1) + C of group
+// tile_group(q >> 1, h), C >= 4 codes 4(q&1) + C - 4 of group tile_group(2 + (q >> 1), h).
+// Each lane's decoded words are its MFMA operand as they are, with no cross-lane moves.
 //   [   0, 1024)  idx stream, bits 0..127 of lane l at 16*l   (dwordx4 per lane)
 //   [1024, 1152)  idx stream, bits 128..143 of lane l at 2*l
-//   [1152, 1664)  sign words of groups 2q, 2q+1 of lane l at 8*l, bit-transposed
-//   [1664, 1728)  scale byte of lane l: low nibble group 2q, high nibble group 2q+1
+//   [1152, 1664)  transposed sign words of lane l's halves h = 0, 1 at 8*l + 4h
+//   [1664, 1728)  scale byte q (scales[q] of the block: groups 2q, 2q+1) of row col at l
 //   [1728, 1760)  fp16 d of row col at 2*col
-// idx stream: code i (0..15, codes 16q..16q+15 of the row) occupies bits [9i, 9i+9) and
-// holds qs | qh_bit << 8. Transposed sign word P of a group: bit (c + 8j) of P is the
-// sign of weight 4c+j, so one rotate places code c's four signs on bits 7,15,23,31.
+// idx stream: slot i occupies bits [9i, 9i+9) and holds qs | qh_bit << 8 of its code.
+// Transposed sign word P of a half: bit (C + 8j) of P is the sign of weight j of slot C,
+// so one rotate places slot C's four signs on bits 7,15,23,31.
 // The bytes are a permutation of the 16 source blocks' bytes (16 x 110 = 1760).
+__host__ __device__ constexpr int tile_group(int kb, int h) { return ((kb & 1) << 2) + ((kb >> 1) << 1) + h; }
 constexpr int kTileRows = 16;
 constexpr int kTileBytes = kTileRows * kIq3sBlockBytes;
 constexpr int kTileIdxA = 0;

@@ -38,6 +38,17 @@ def test_soa_fields_preserve_every_byte(gpu, n_rows, blocks):
     np.testing.assert_array_equal(unpack_tiles(fields.packed.cpu().numpy(), n_rows, blocks), raw)
 
 
+def _tile_group(kb: int, h: int) -> int:
+    """Weight group in K block kb of MFMA half h (tile layout in mambo_amd/csrc/mambo_common.h)."""
+    return ((kb & 1) << 2) + ((kb >> 1) << 1) + h
+
+
+def _slot_code(q: int, i: int) -> int:
+    """Code (0..63) of the block held in slot i (0..15) of lane group q."""
+    h, c = i >> 3, i & 7
+    return 8 * _tile_group(2 * (c >> 2) + (q >> 1), h) + 4 * (q & 1) + (c & 3)
+
+
 def unpack_tiles(packed: np.ndarray, n: int, blocks: int) -> np.ndarray:
     """Inverse of the 16-row x 1-block tile layout (mambo_amd/csrc/mambo_common.h)."""
     tiles = (n + 15) // 16
@@ -49,7 +60,7 @@ def unpack_tiles(packed: np.ndarray, n: int, blocks: int) -> np.ndarray:
         tail = p[:, :, 1024 + 2 * lane:1026 + 2 * lane].copy().view("<u2").astype(np.uint64)
         w = [words[..., i] for i in range(4)] + [tail[..., 0], np.zeros_like(tail[..., 0])]
         for i in range(16):
-            c = 16 * q + i
+            c = _slot_code(q, i)
             pos = 9 * i
             wi, sh = pos // 32, pos % 32
             val = ((w[wi] >> np.uint64(sh)) | (w[wi + 1] << np.uint64(32 - sh))) & np.uint64(0x1FF)
@@ -57,12 +68,12 @@ def unpack_tiles(packed: np.ndarray, n: int, blocks: int) -> np.ndarray:
             raw[:, r, :, 66 + c // 8] |= ((val >> np.uint64(8)).astype(np.uint8) << np.uint8(c % 8))
         for h in range(2):
             t = p[:, :, 1152 + 8 * lane + 4 * h:1152 + 8 * lane + 4 * h + 4].copy().view("<u4")[..., 0]
-            sw = np.zeros_like(t)
             for c in range(8):
+                code = _slot_code(q, 8 * h + c)
                 for j in range(4):
-                    sw |= ((t >> np.uint32(c + 8 * j)) & np.uint32(1)) << np.uint32(4 * c + j)
-            raw[:, r, :, 74 + 4 * (2 * q + h):78 + 4 * (2 * q + h)] = sw[..., None].view(np.uint8).reshape(
-                tiles, blocks, 4)
+                    bit = ((t >> np.uint32(c + 8 * j)) & np.uint32(1)).astype(np.uint8)
+                    k = 4 * code + j
+                    raw[:, r, :, 74 + k // 8] |= bit << np.uint8(k % 8)
         raw[:, r, :, 106 + q] = p[:, :, 1664 + lane]
         if q == 0:
             raw[:, r, :, 0:2] = p[:, :, 1728 + 2 * r:1730 + 2 * r]
