@@ -134,3 +134,32 @@ def test_row_strided_scales_through_the_tiled_kernel(gpu):
         torch.cuda.synchronize()
         check(out.cpu().numpy(), expected)
         check(ref.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_odd_scale_rows_through_the_stream_kernel(gpu, m):
+    """C ABI call at 1 and 3 tokens with the activation scale rows at an odd address and
+    an odd row stride (K/32 + 1 bytes): the stream kernel then reads the scales from
+    global memory a byte at a time (its LDS copy moves them as dwords, so it is not
+    used); the result matches the oracle."""
+    from mambo_amd import _native
+    from mambo_amd.utils.iq3_s_weight import ensure_packed, prepare_iq3_s_fields
+    n, k = 256, 4096
+    raw = oracle.gen_iq3s(57, n, k // 256)
+    packed = ensure_packed(prepare_iq3_s_fields(torch.from_numpy(raw).to(gpu), fields=False))
+    xv, xs = oracle.quantize_mxfp8(np.random.default_rng(30 + m).standard_normal((m, k)).astype(np.float32))
+    xvg = torch.from_numpy(xv).to(gpu)
+    ld = k // 32 + 1
+    buf = torch.zeros(1 + m * ld, dtype=torch.uint8, device=gpu)
+    scales = buf[1:].view(m, ld)
+    scales[:, :k // 32] = torch.from_numpy(xs).to(gpu)
+    assert scales.data_ptr() % 2 == 1 and ld % 2 == 1
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=gpu)
+    cfg = _native.GemmConfig.from_dict({"kernel": _native.GEMM_STREAM, "waves": 4, "split_k": 1, "tile_n": 16})
+    lib = _native.lib()
+    step(f"matmul M={m} scales at an odd address, row stride {ld}")
+    rc = lib.mambo_iq3s_fp8_matmul(xvg.data_ptr(), k, scales.data_ptr(), ld, m, packed.data_ptr(), n, k // 256,
+                                   out.data_ptr(), n, ctypes.byref(cfg), None)
+    assert rc == 0, lib.mambo_last_error()
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), oracle.iq3s_fp8_matmul(xv, xs, raw, threads=oracle.default_threads()))
