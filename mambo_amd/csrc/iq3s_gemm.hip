@@ -396,7 +396,8 @@ __host__ __device__ inline DenseLds dense_lds(int W, int NT, int MC, int rows, i
 // per token drops by MC). Grouped projections start on a workgroup boundary
 // (tile_begin counts workgroups).
 template <int W, int NT, bool kLdsAct, int MC>
-__global__ __launch_bounds__(W * 64) void gemm_dense_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dense_kernel(
+    const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
 {
@@ -774,7 +775,8 @@ __device__ __forceinline__ void mfma_half(const uint8_t *buf, const uint32_t (&a
 // its own block per step, so a workgroup of the same weight rows holds kKs times the
 // waves; the groups' sums are added through LDS in group order at the end.
 template <int MT, int NT, int W, bool kHalf = false, int kKs = 1>
-__global__ __launch_bounds__(W * 64) void gemm_tiled_kernel(const uint8_t *__restrict__ xv, int64_t ldxv,
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_tiled_kernel(
+    const uint8_t *__restrict__ xv, int64_t ldxv,
                                                             const uint8_t *__restrict__ xs, int64_t ldxs, int64_t M,
                                                             GroupArgs ga, int B, int bps, int atomic)
 {
