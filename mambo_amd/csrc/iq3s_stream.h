@@ -98,7 +98,7 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 
 // One lane's share of a tile-block (load_w_rsrc): the block at byte `step` past the
 // resource base, in kWLoads vector memory instructions (codes b128 + b16, signs b64,
-// scale nibbles b8 or b16, the row's fp16 d b16).
+// the scale byte b8, the row's fp16 d b16).
 constexpr int kWLoads = 5;
 // Cache policy of the decode kernels' weight loads: non-temporal (gfx940-family CPol NT
 // bit). Each weight byte is read once per launch; marking the stream for early eviction
